@@ -1,0 +1,147 @@
+/*
+ * strata_mi355x.h - C ABI of the MI355X (gfx950) mixture-of-experts library
+ * (libstrata_mi355x.so). Plain integers, pointers and sizes only.
+ *
+ * Device buffers are identified by handles: the device address returned by
+ * sm_alloc. The library records the size of every allocation and checks each
+ * launch's accesses against those sizes on the host before anything runs;
+ * a handle that sm_alloc did not return is rejected.
+ *
+ * Return codes: 0 on success, a negative SM_E* value on failure; the message
+ * of the last failure on a context is sm_last_error(ctx).
+ *
+ * Ordering: every call on one context is issued in order on that context's
+ * HIP stream (default priority). sm_read waits for the copy; sm_write waits
+ * until the host source may be reused; everything else is asynchronous until
+ * sm_sync. One context must not be used from two threads at once.
+ *
+ * Reference interfaces each entry replaces (file:line in SamG-Coder/StrataCuda):
+ *   sm_alloc / sm_free / sm_write / sm_read / sm_copy / sm_zero / sm_sync
+ *       GpuBackend.alloc/free/write/read/copy/zero/idle, src/backend.js:84-119;
+ *       WasmBackend, src/backend.js:128-149; ThreadedProgram.alloc/write/read,
+ *       vendor/webcuda/src/wasm/runtime.js:7-9
+ *   sm_run
+ *       backend.run(name, args, groups), src/backend.js:101-113 and :144;
+ *       the per-entry C ABI cw_<entry>(gx, gy, gz, params...),
+ *       vendor/webcuda/src/wasm/compile.mjs:37, dispatched by
+ *       ThreadedProgram.dispatch, vendor/webcuda/src/wasm/runtime.js:10-15
+ *   sm_moe_route / sm_moe_dispatch / sm_moe_layer / sm_moe_layer_workspace
+ *       the MoE stage driven from JavaScript by StrataEngine.moe,
+ *       src/engine.js:133-156 (decode), and PromptBatch.moe,
+ *       src/prefill.js:52-78 (prompt): router projection, strata_router,
+ *       host grouping, per-expert strata_q2_gate_up / strata_q2_down,
+ *       shared expert, shared gate and strata_moe_combine, done on the device
+ *       without a host readback of the routed IDs
+ *   sm_synth_*
+ *       no reference counterpart: seeded synthetic inputs for tests and the
+ *       benchmark, generated on the device
+ */
+#ifndef STRATA_MI355X_H
+#define STRATA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SM_OK 0
+#define SM_E_HIP (-1)        /* a HIP runtime call failed */
+#define SM_E_ARG (-2)        /* invalid argument (RangeError in the reference) */
+#define SM_E_BOUNDS (-3)     /* an access would leave a buffer (buffer layout error) */
+#define SM_E_HANDLE (-4)     /* not a live handle of this context */
+#define SM_E_NOKERNEL (-5)   /* unknown kernel name (src/backend.js:103) */
+#define SM_E_ROUTE (-6)      /* invalid routing result detected on the device */
+#define SM_E_NOMEM (-7)      /* allocation failed */
+
+typedef struct sm_ctx sm_ctx;
+
+/* ---------------------------------------------------------------- context */
+int sm_init(int device, sm_ctx **out);
+void sm_shutdown(sm_ctx *ctx);
+const char *sm_last_error(sm_ctx *ctx);
+/* Writes a JSON object describing the device and counters (GpuBackend.info,
+ * src/backend.js:120) into buf; returns the length or a negative code. */
+int sm_info(sm_ctx *ctx, char *buf, size_t cap);
+
+/* ---------------------------------------------------------------- buffers */
+int sm_alloc(sm_ctx *ctx, uint64_t bytes, int zero, uint64_t *handle);
+int sm_free(sm_ctx *ctx, uint64_t handle);
+int sm_size(sm_ctx *ctx, uint64_t handle, uint64_t *bytes);
+int sm_write(sm_ctx *ctx, uint64_t dst, uint64_t dst_offset, const void *src, uint64_t bytes);
+int sm_read(sm_ctx *ctx, uint64_t src, uint64_t src_offset, void *dst, uint64_t bytes);
+int sm_copy(sm_ctx *ctx, uint64_t src, uint64_t src_offset, uint64_t dst, uint64_t dst_offset,
+            uint64_t bytes);
+int sm_zero(sm_ctx *ctx, uint64_t dst, uint64_t offset, uint64_t bytes);
+int sm_sync(sm_ctx *ctx);
+
+/* ------------------------------------------------------ kernels by name */
+/* Launch a reference kernel by name with the reference's grid semantics:
+ * groups = {gx, gy, gz} workgroups of 64 lanes (scripts/build.mjs:10).
+ * args holds one 64-bit slot per parameter in the reference's parameter order:
+ * a buffer handle for pointer parameters, the int32 or float32 bit pattern in
+ * the low 32 bits for scalars. sm_kernel_signature gives the parameter list
+ * as "Name:type,..." with types f32*, i32*, u32*, i32 and f32. */
+int sm_run(sm_ctx *ctx, const char *name, const uint32_t groups[3], const uint64_t *args, int nargs);
+int sm_kernel_count(void);
+const char *sm_kernel_name(int index);
+const char *sm_kernel_signature(const char *name);
+
+/* ----------------------------------------------------------- MoE layer */
+/* Router: logits[t, e] = X[t,:] . Wr[e,:] (+ bias[e] when bias != 0) in the
+ * reference's f32 operation order, then softmax, top-k by repeated argmax
+ * (lower ID wins ties) and renormalisation (kernels/strata.cu:156-165,
+ * 240-270, 479-509). logits may be 0 when not wanted.
+ * X [tokens x width] f32, Wr [experts x width] f32, ids/weights [tokens x topk]. */
+int sm_moe_route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t bias, int experts,
+                 int topk, uint64_t logits, uint64_t ids, uint64_t weights);
+
+/* Expert-contiguous dispatch of routed IDs: experts ascending, tokens
+ * ascending within an expert (the within-expert order of src/prefill.js:56-61).
+ * offsets [experts+1] exclusive scan of counts; rows[pos] = token;
+ * parts[pos] = token*topk + k; where[token*topk + k] = pos. Fails with
+ * SM_E_ROUTE if an ID is out of range or repeated within a token
+ * (src/engine.js:138, src/prefill.js:57). */
+int sm_moe_dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets,
+                    uint64_t rows, uint64_t parts, uint64_t where_, uint64_t workspace,
+                    uint64_t workspace_bytes);
+
+/* One MoE layer: Y = sigmoid(X . Wsg) * Shared(X) + sum_k w_k * Expert_{id_k}(X)
+ * per token. Expert e's Q2 blob starts at arena + e*blob_stride; the shared
+ * expert's blob is shared_blob. Blob layout (vendor/strata/tools/pack_layer.py:54-65):
+ * gate/up codes (2*ff interleaved rows of width/4 B), down codes (width rows of
+ * ff/4 B), gate/up fp16 scales, down fp16 scales; 64-weight groups; weight =
+ * (code - 1) * scale. width and ff must be multiples of 64.
+ * ids/weights (tokens x topk) receive the routing. workspace must hold
+ * sm_moe_layer_workspace(...) bytes. tokens == 1 runs the decode kernels
+ * (GEMV); tokens > 1 runs dispatch + grouped MFMA GEMMs. */
+int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes);
+int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
+                 uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
+                 int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,
+                 uint64_t workspace_bytes);
+
+/* ---------------------------------------------------------------- timing */
+/* Events on the context's stream (the stream every launch above uses). */
+int sm_event_record(sm_ctx *ctx, int slot);          /* slot in [0, 64) */
+int sm_event_elapsed(sm_ctx *ctx, int start_slot, int end_slot, float *ms);
+
+/* ------------------------------------------------------ synthetic inputs */
+/* No reference counterpart. Deterministic seeded data, bit-identical to the
+ * CPU oracle's generator:
+ *   sm_synth_normal: f32 values sigma * normal(seed, stream, i)
+ *   sm_synth_uniform_pm: f32 values 1 + amp * U(-1, 1)
+ *   sm_synth_blobs: `count` Q2 blobs at dst + i*stride, blob i from stream
+ *                   first_stream + i (codes uniform, scales fp16(|sigma*N|)) */
+int sm_synth_normal(sm_ctx *ctx, uint64_t dst, uint64_t offset_bytes, uint64_t n, uint64_t seed,
+                    uint64_t stream, double sigma);
+int sm_synth_uniform_pm(sm_ctx *ctx, uint64_t dst, uint64_t offset_bytes, uint64_t n, uint64_t seed,
+                        uint64_t stream, double amp);
+int sm_synth_blobs(sm_ctx *ctx, uint64_t dst, uint64_t offset_bytes, uint64_t stride, int count, int width,
+                   int ff, uint64_t seed, uint64_t first_stream, double sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* STRATA_MI355X_H */

@@ -1,0 +1,78 @@
+"""Builds libstrata_mi355x.so (HIP, gfx950) and the Node-API addon in-tree.
+
+Every HIP source is compiled with
+  --offload-arch=gfx950 -O3 -ffp-contract=off
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+-ffp-contract=off keeps each f32 product and sum separately rounded unless a
+kernel asks for fmaf explicitly (the router and the reference-named kernels
+depend on it for bit-exact results); packed FP32 instructions are disabled.
+"""
+import concurrent.futures
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+ROOT = os.path.dirname(HERE)
+INCLUDE = os.path.join(ROOT, "include")
+LIB = os.path.join(HERE, "libstrata_mi355x.so")
+ADDON = os.path.join(HERE, "src", "strata_addon.node")
+OBJ = os.path.join(HERE, "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_SOURCES = ["kernels_ref.hip", "moe_route.hip", "moe_decode.hip", "moe_prefill.hip", "synth.hip"]
+HOST_SOURCES = ["runtime.cpp"]
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-Wall",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError("command failed: %s\n%s" % (" ".join(cmd), out))
+    return out
+
+
+def build_library(jobs=8):
+    os.makedirs(OBJ, exist_ok=True)
+    cmds = []
+    for src in HIP_SOURCES:
+        cmds.append([HIPCC] + HIP_FLAGS + ["-I", INCLUDE, "-c", os.path.join(CSRC, src), "-o",
+                                            os.path.join(OBJ, src + ".o")])
+    for src in HOST_SOURCES:
+        cmds.append([HIPCC, "-O2", "-fPIC", "-std=c++17", "-Wall", "-I", INCLUDE, "-c", os.path.join(CSRC, src),
+                     "-o", os.path.join(OBJ, src + ".o")])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for out in ex.map(_run, cmds):
+            if out.strip():
+                sys.stderr.write(out + "\n")
+    objs = [os.path.join(OBJ, s + ".o") for s in HIP_SOURCES + HOST_SOURCES]
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_addon():
+    """Node-API addon (C ABI wrapper for the JavaScript host), if node headers exist."""
+    src = os.path.join(CSRC, "addon.cc")
+    if not os.path.exists(src) or not os.path.exists("/usr/include/node/node_api.h"):
+        return None
+    tmp = ADDON + ".tmp"
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-DNAPI_VERSION=8", "-I/usr/include/node",
+          "-I", INCLUDE, "-o", tmp, src, "-L", HERE, "-lstrata_mi355x", "-Wl,-rpath,$ORIGIN/..",
+          "-Wl,--unresolved-symbols=ignore-in-shared-libs"])
+    os.replace(tmp, ADDON)
+    return ADDON
+
+
+def build():
+    build_library()
+    build_addon()
+
+
+if __name__ == "__main__":
+    build()
+    print(LIB)

@@ -1,0 +1,68 @@
+// Host-side internals shared by the library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+
+#include "../../include/strata_mi355x.h"
+
+struct sm_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::map<uint64_t, uint64_t> buffers;  // handle (device address) -> bytes
+    std::string error;
+    hipEvent_t events[64] = {};
+    // Device words used by kernels that elect their last-arriving workgroup
+    // (route completion counters). Each kernel returns its counter to zero.
+    uint32_t *counters = nullptr;
+    uint64_t launches = 0, bytes_written = 0, bytes_read = 0, allocated = 0;
+};
+
+namespace smi {
+
+int fail(sm_ctx *ctx, int code, const std::string &msg);
+int hip_fail(sm_ctx *ctx, hipError_t err, const char *what);
+// Checks that `handle` is a live allocation holding at least `bytes` bytes.
+int need(sm_ctx *ctx, uint64_t handle, uint64_t bytes, const char *what);
+int launched(sm_ctx *ctx);  // checks hipGetLastError after a launch
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Launchers defined in the kernel translation units.
+int route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t bias, int experts, int topk,
+          uint64_t logits, uint64_t ids, uint64_t weights, uint64_t gate_w, uint64_t gate_out);
+// Unchecked launchers on raw device pointers (callers validated the buffers).
+int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float *Wr, const float *bias, int experts,
+                 int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out);
+int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int experts, int *offsets, int *rows, int *parts,
+                    int *where_, char *workspace, int extra_rows, int *tile_base_out);
+int dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets, uint64_t rows,
+             uint64_t parts, uint64_t where_, uint64_t workspace, uint64_t workspace_bytes, int extra_rows);
+uint64_t dispatch_workspace(int tokens, int experts);
+int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
+               uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y,
+               uint64_t ids, uint64_t weights, uint64_t workspace, uint64_t workspace_bytes);
+uint64_t moe_decode_workspace(int width, int ff, int experts, int topk);
+int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
+                uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
+                int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,
+                uint64_t workspace_bytes);
+uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk);
+
+// Byte sizes of the regions of one Q2 expert blob.
+struct BlobLayout {
+    uint64_t gate_up_codes, down_codes, gate_up_scales, down_scales, bytes;
+};
+inline BlobLayout blob_layout(int width, int ff) {
+    BlobLayout L;
+    L.gate_up_codes = 0;
+    L.down_codes = (uint64_t)2 * ff * width / 4;
+    L.gate_up_scales = L.down_codes + (uint64_t)width * ff / 4;
+    L.down_scales = L.gate_up_scales + (uint64_t)2 * ff * (width / 64) * 2;
+    L.bytes = L.down_scales + (uint64_t)width * (ff / 64) * 2;
+    return L;
+}
+
+}  // namespace smi

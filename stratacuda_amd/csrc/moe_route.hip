@@ -1,0 +1,357 @@
+// Router logits, softmax top-k and expert-contiguous dispatch on the device.
+//
+// Router logits follow the reference's f32 operation order exactly
+// (kernels/strata.cu:156-165: lane l sums columns l, l+64, ... in order, then
+// the tree s = 32..1), so selected expert IDs and their order are bit-exact
+// with the reference's CPU path; the top-k is router_wave (strata.cu:240-270).
+//
+//  * tokens == 1: one wave per router row; the last wave to finish (elected
+//    with a device-scope counter) runs the top-k, so routing is one launch.
+//  * tokens > 1: register-tiled exact GEMM. Each wave owns 8 tokens x 8 rows
+//    and keeps, per lane l, the 64 partial sums of "lane l" of the reference
+//    workgroup for all 64 outputs. A transpose (butterfly) reduction then
+//    forms the reference tree for every output: at level s each lane keeps
+//    half of its outputs and adds its partner's (lane ^ s) copy, which yields
+//    exactly partial[l] + partial[l+s] of the reference (f32 addition is
+//    commutative), and after six levels lane l holds output l.
+//
+// Dispatch (replacing the host grouping of src/prefill.js:56-61): per block of
+// 64 tokens a 64-bit token mask per expert, an exclusive scan over
+// (expert, block) in expert-major order, and the rank of a token inside its
+// expert = base + popcount of the lower mask bits. Integer-only, so the
+// permutation (experts ascending, tokens ascending within an expert) is
+// deterministic.
+#include <hip/hip_runtime.h>
+
+#include "internal.h"
+#include "strata_device.h"
+
+using namespace smi;
+
+namespace {
+
+// ------------------------------------------------------------ T = 1 route
+// Rows [0, experts) are router rows, row `experts` is the shared-expert gate
+// (when gate_w != 0). One 64-thread block per row.
+__global__ void __launch_bounds__(64) k_route_t1(const float *__restrict__ X, const float *__restrict__ Wr,
+                                                 const float *__restrict__ bias, const float *__restrict__ Wsg,
+                                                 float *__restrict__ logits, float *__restrict__ gate_out,
+                                                 int *__restrict__ ids, float *__restrict__ weights, int width,
+                                                 int experts, int topk, uint32_t *counter, int total_rows) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const float *w = row < experts ? Wr + (int64_t)row * width : Wsg;
+    float sum = 0.0f;
+    int i = lane;
+    // 4 independent loads in flight per iteration; the sum stays sequential.
+    for (; i + 192 < width; i += 256) {
+        float w0 = w[i], w1 = w[i + 64], w2 = w[i + 128], w3 = w[i + 192];
+        float x0 = X[i], x1 = X[i + 64], x2 = X[i + 128], x3 = X[i + 192];
+        sum = sum + w0 * x0;
+        sum = sum + w1 * x1;
+        sum = sum + w2 * x2;
+        sum = sum + w3 * x3;
+    }
+    for (; i < width; i += 64) sum = sum + w[i] * X[i];
+    sum = sm::tree_sum64(sum);
+    if (lane == 0) {
+        if (row < experts) logits[row] = bias ? sum + bias[row] : sum;
+        else gate_out[0] = sum;
+    }
+    // Elect the last row to finish; it runs the top-k over all logits.
+    __threadfence();
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0, 64);
+    if (old != (uint32_t)total_rows - 1) return;
+    __threadfence();
+    sm::router_wave(logits, ids, weights, experts, topk);
+    if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// -------------------------------------------------------- T > 1 route GEMM
+constexpr int TT = 8, TR = 8;  // tokens x rows per wave
+
+template <int N>
+__device__ __forceinline__ void butterfly_level(float (&a)[64], int lane) {
+    // N = number of outputs still held; keeps N/2.
+    constexpr int H = N / 2;
+    const bool upper = (lane & H) != 0;
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+        float send = upper ? a[i] : a[i + H];
+        float keep = upper ? a[i + H] : a[i];
+        a[i] = keep + __shfl_xor(send, H, 64);
+    }
+}
+
+// Grid: x = row tiles (ceil((experts+1)/8)), y = token tiles (ceil(T/8)).
+// Row `experts` is the shared-expert gate. Rows/tokens past the end are
+// computed on clamped (valid) addresses and discarded.
+__global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X, const float *__restrict__ Wr,
+                                                    const float *__restrict__ bias, const float *__restrict__ Wsg,
+                                                    float *__restrict__ logits, float *__restrict__ gate_out,
+                                                    int tokens, int width, int experts, int with_gate) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nrows = experts + (with_gate ? 1 : 0);
+    const int row_tiles = (nrows + TR - 1) / TR;
+    const int tile = blockIdx.x * 4 + wave;
+    if (tile >= row_tiles) return;
+    const int r0 = tile * TR, t0 = blockIdx.y * TT;
+    const float *wp[TR];
+    const float *xp[TT];
+#pragma unroll
+    for (int r = 0; r < TR; r++) {
+        int row = min(r0 + r, nrows - 1);
+        wp[r] = row < experts ? Wr + (int64_t)row * width : Wsg;
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) xp[t] = X + (int64_t)min(t0 + t, tokens - 1) * width;
+    float a[64];
+#pragma unroll
+    for (int o = 0; o < 64; o++) a[o] = 0.0f;
+    for (int i = lane; i < width; i += 64) {
+        float xv[TT], wv[TR];
+#pragma unroll
+        for (int t = 0; t < TT; t++) xv[t] = xp[t][i];
+#pragma unroll
+        for (int r = 0; r < TR; r++) wv[r] = wp[r][i];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < TR; r++) a[t * TR + r] = a[t * TR + r] + wv[r] * xv[t];
+    }
+    butterfly_level<64>(a, lane);
+    butterfly_level<32>(a, lane);
+    butterfly_level<16>(a, lane);
+    butterfly_level<8>(a, lane);
+    butterfly_level<4>(a, lane);
+    butterfly_level<2>(a, lane);
+    // lane l now holds output o = l: token t0 + l/8, row r0 + l%8.
+    const int t = t0 + lane / TR, row = r0 + lane % TR;
+    if (t < tokens && row < nrows) {
+        if (row < experts) logits[(int64_t)t * experts + row] = bias ? a[0] + bias[row] : a[0];
+        else gate_out[t] = a[0];
+    }
+}
+
+__global__ void __launch_bounds__(256) k_topk(const float *__restrict__ logits, int *__restrict__ ids,
+                                              float *__restrict__ weights, int tokens, int experts, int topk) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    sm::router_wave(logits + (int64_t)t * experts, ids + (int64_t)t * topk, weights + (int64_t)t * topk, experts, topk);
+}
+
+// ---------------------------------------------------------------- dispatch
+// Block b covers tokens [64b, 64b+64). masks[b*E + e] = tokens of the block
+// routed to e; counts[e*nb + b] = popcount. status bit 0: an ID outside
+// [0, experts); bit 1: an ID repeated within one token.
+__global__ void __launch_bounds__(256) k_dispatch_masks(const int *__restrict__ ids, int tokens, int topk, int experts,
+                                                        int nb, unsigned long long *__restrict__ masks,
+                                                        int *__restrict__ counts, uint32_t *status) {
+    __shared__ unsigned long long m[512];
+    const int b = blockIdx.x;
+    for (int e = threadIdx.x; e < experts; e += blockDim.x) m[e] = 0ull;
+    __syncthreads();
+    const int t0 = b * 64, nt = min(64, tokens - t0);
+    for (int a = threadIdx.x; a < nt * topk; a += blockDim.x) {
+        int tl = a / topk, e = ids[(int64_t)(t0 + tl) * topk + a % topk];
+        if (e < 0 || e >= experts) {
+            atomicOr(status, 1u);
+            continue;
+        }
+        unsigned long long bit = 1ull << tl;
+        unsigned long long old = atomicOr(&m[e], bit);
+        if (old & bit) atomicOr(status, 2u);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+        masks[(int64_t)b * experts + e] = m[e];
+        counts[(int64_t)e * nb + b] = __popcll(m[e]);
+    }
+}
+
+// Single block: exclusive scan of counts (expert-major) into base, per-expert
+// offsets[E+1] (+ offsets[E+1] = offsets[E] + extra for the shared-expert
+// segment), and m-tile bases for the grouped GEMMs: tile_base[s] = sum over
+// segments s' < s of ceil(n_s' / mt) (segments = experts, then the extra one).
+__global__ void __launch_bounds__(1024) k_dispatch_scan(const int *__restrict__ counts, int *__restrict__ base,
+                                                        int *__restrict__ offsets, int *__restrict__ tile_base,
+                                                        int experts, int nb, int extra, int mt) {
+    __shared__ int part[1024];
+    __shared__ int seg[513];
+    const int n = experts * nb, tid = threadIdx.x;
+    const int chunk = (n + 1023) / 1024, lo = min(n, tid * chunk), hi = min(n, lo + chunk);
+    int s = 0;
+    for (int i = lo; i < hi; i++) s += counts[i];
+    part[tid] = s;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {
+        int v = tid >= d ? part[tid - d] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    int run = tid ? part[tid - 1] : 0;
+    for (int i = lo; i < hi; i++) {
+        base[i] = run;
+        run += counts[i];
+    }
+    __syncthreads();
+    const int total = part[1023];
+    for (int e = tid; e < experts; e += 1024) offsets[e] = base[(int64_t)e * nb];
+    if (tid == 0) {
+        offsets[experts] = total;
+        offsets[experts + 1] = total + extra;
+    }
+    __syncthreads();
+    // Tile bases over experts + 1 segments (the last may be empty).
+    for (int e = tid; e <= experts; e += 1024) {
+        int cnt = offsets[e + 1] - offsets[e];
+        seg[e] = (cnt + mt - 1) / mt;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e <= experts; e++) {
+            tile_base[e] = acc;
+            acc += seg[e];
+        }
+        tile_base[experts + 1] = acc;
+    }
+}
+
+__global__ void k_dispatch_place(const int *__restrict__ ids, int tokens, int topk, int experts, int nb,
+                                 const unsigned long long *__restrict__ masks, const int *__restrict__ base,
+                                 int *__restrict__ rows, int *__restrict__ parts, int *__restrict__ where_,
+                                 int extra, const int *__restrict__ offsets) {
+    const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n = (int64_t)tokens * topk;
+    if (a < n) {
+        int t = (int)(a / topk), e = ids[a];
+        if (e < 0 || e >= experts) {
+            where_[a] = -1;
+            return;
+        }
+        int b = t >> 6, tl = t & 63;
+        unsigned long long below = tl ? (masks[(int64_t)b * experts + e] & ((1ull << tl) - 1ull)) : 0ull;
+        int pos = base[(int64_t)e * nb + b] + __popcll(below);
+        rows[pos] = t;
+        parts[pos] = (int)a;
+        where_[a] = pos;
+    } else if (extra && a < n + tokens) {
+        // The shared-expert segment follows the routed rows (offsets[experts]).
+        int t = (int)(a - n), at = offsets[experts] + t;
+        rows[at] = t;
+        parts[at] = -1;
+    }
+}
+
+// ---------------------------------------------------------- workspace
+constexpr uint64_t kAlign = 256;
+constexpr int kGemmMT = 32;  // token rows per grouped-GEMM tile (moe_prefill.hip)
+inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct DispatchWs {
+    uint64_t status, masks, counts, base, tile_base, end;
+};
+DispatchWs dispatch_ws(int tokens, int experts) {
+    const uint64_t nb = (uint64_t)(tokens + 63) / 64;
+    DispatchWs w;
+    w.status = 0;
+    w.masks = up(w.status + 64);
+    w.counts = up(w.masks + nb * experts * 8);
+    w.base = up(w.counts + nb * experts * 4);
+    w.tile_base = up(w.base + nb * experts * 4);
+    w.end = up(w.tile_base + ((uint64_t)experts + 2) * 4);
+    return w;
+}
+
+}  // namespace
+
+namespace smi {
+
+uint64_t dispatch_workspace(int tokens, int experts) { return dispatch_ws(tokens, experts).end; }
+
+int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float *Wr, const float *bias, int experts,
+                 int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out) {
+    if (tokens == 1) {
+        const int total = experts + (gate_w ? 1 : 0);
+        k_route_t1<<<total, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, ids, weights, width, experts,
+                                                  topk, ctx->counters + 0, total);
+        return launched(ctx);
+    }
+    const int nrows = experts + (gate_w ? 1 : 0);
+    dim3 grid((unsigned)ceil_div(ceil_div(nrows, TR), 4), (unsigned)ceil_div(tokens, TT));
+    k_route_gemm<<<grid, 256, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, tokens, width, experts,
+                                                gate_w ? 1 : 0);
+    if (int rc = launched(ctx)) return rc;
+    k_topk<<<ceil_div(tokens, 4), 256, 0, ctx->stream>>>(logits, ids, weights, tokens, experts, topk);
+    return launched(ctx);
+}
+
+int route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t bias, int experts, int topk,
+          uint64_t logits, uint64_t ids, uint64_t weights, uint64_t gate_w, uint64_t gate_out) {
+    if (int rc = need(ctx, X, (uint64_t)tokens * width * 4, "X")) return rc;
+    if (int rc = need(ctx, Wr, (uint64_t)experts * width * 4, "router weights")) return rc;
+    if (bias)
+        if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
+    if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
+    if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
+    if (gate_w) {
+        if (int rc = need(ctx, gate_w, (uint64_t)width * 4, "shared gate weights")) return rc;
+        if (int rc = need(ctx, gate_out, (uint64_t)tokens * 4, "shared gate output")) return rc;
+    }
+    uint64_t L = logits;
+    bool own = false;
+    if (!L) {  // the caller does not keep the logits: use a temporary
+        if (int rc = sm_alloc(ctx, (uint64_t)tokens * experts * 4, 0, &L)) return rc;
+        own = true;
+    } else if (int rc = need(ctx, L, (uint64_t)tokens * experts * 4, "logits")) {
+        return rc;
+    }
+    int rc = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts, topk,
+                          (float *)L, (int *)ids, (float *)weights, (const float *)gate_w, (float *)gate_out);
+    if (own) {
+        int rc2 = sm_free(ctx, L);
+        if (!rc) rc = rc2;
+    }
+    return rc;
+}
+
+int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int experts, int *offsets, int *rows, int *parts,
+                    int *where_, char *ws, int extra_rows, int *tile_base_out) {
+    const int nb = ceil_div(tokens, 64);
+    DispatchWs w = dispatch_ws(tokens, experts);
+    const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
+    hipError_t e = hipMemsetAsync(ws + w.status, 0, 64, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMemsetAsync");
+    k_dispatch_masks<<<nb, 256, 0, ctx->stream>>>(ids, tokens, topk, experts, nb, (unsigned long long *)(ws + w.masks),
+                                                  (int *)(ws + w.counts), (uint32_t *)(ws + w.status));
+    if (int rc = launched(ctx)) return rc;
+    int *tile_base = tile_base_out ? tile_base_out : (int *)(ws + w.tile_base);
+    k_dispatch_scan<<<1, 1024, 0, ctx->stream>>>((const int *)(ws + w.counts), (int *)(ws + w.base), offsets, tile_base,
+                                                 experts, nb, (int)extra, kGemmMT);
+    if (int rc = launched(ctx)) return rc;
+    const uint64_t threads = n + extra;
+    k_dispatch_place<<<(unsigned)((threads + 255) / 256), 256, 0, ctx->stream>>>(
+        ids, tokens, topk, experts, nb, (const unsigned long long *)(ws + w.masks), (const int *)(ws + w.base), rows,
+        parts, where_, (int)extra, offsets);
+    return launched(ctx);
+}
+
+int dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets, uint64_t rows,
+             uint64_t parts, uint64_t where_, uint64_t workspace, uint64_t workspace_bytes, int extra_rows) {
+    DispatchWs w = dispatch_ws(tokens, experts);
+    const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
+    if (workspace_bytes < w.end) return fail(ctx, SM_E_ARG, "dispatch workspace too small");
+    if (int rc = need(ctx, workspace, w.end, "dispatch workspace")) return rc;
+    if (int rc = need(ctx, ids, n * 4, "ids")) return rc;
+    if (int rc = need(ctx, offsets, ((uint64_t)experts + 2) * 4, "offsets")) return rc;
+    if (int rc = need(ctx, rows, (n + extra) * 4, "rows")) return rc;
+    if (int rc = need(ctx, parts, (n + extra) * 4, "parts")) return rc;
+    if (int rc = need(ctx, where_, n * 4, "where")) return rc;
+    return dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, (int *)offsets, (int *)rows, (int *)parts,
+                           (int *)where_, (char *)workspace, extra_rows, nullptr);
+}
+
+}  // namespace smi

@@ -1,0 +1,266 @@
+// Context, buffer registry, copies, events and the MoE entry points of
+// libstrata_mi355x.so. Every device buffer the library touches is an
+// allocation it made, so every launch is bounds-checked on the host first.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "internal.h"
+
+namespace smi {
+
+int fail(sm_ctx *ctx, int code, const std::string &msg) {
+    if (ctx) ctx->error = msg;
+    return code;
+}
+
+int hip_fail(sm_ctx *ctx, hipError_t err, const char *what) {
+    return fail(ctx, SM_E_HIP, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+int need(sm_ctx *ctx, uint64_t handle, uint64_t bytes, const char *what) {
+    auto it = ctx->buffers.find(handle);
+    if (it == ctx->buffers.end())
+        return fail(ctx, SM_E_HANDLE, std::string(what) + ": not a live buffer of this context");
+    if (it->second < bytes)
+        return fail(ctx, SM_E_BOUNDS, std::string(what) + ": needs " + std::to_string(bytes) + " bytes, buffer has " +
+                                          std::to_string(it->second));
+    return SM_OK;
+}
+
+int launched(sm_ctx *ctx) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return hip_fail(ctx, err, "kernel launch");
+    ctx->launches++;
+    return SM_OK;
+}
+
+}  // namespace smi
+
+using namespace smi;
+
+#define HIP_TRY(ctx, call)                                    \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+    } while (0)
+
+extern "C" {
+
+int sm_init(int device, sm_ctx **out) {
+    if (!out) return SM_E_ARG;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return SM_E_HIP;
+    if (device < 0 || device >= count) return SM_E_ARG;
+    sm_ctx *ctx = new sm_ctx();
+    ctx->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return SM_E_HIP;
+    }
+    for (auto &e : ctx->events) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            sm_shutdown(ctx);
+            return SM_E_HIP;
+        }
+    }
+    if (hipMalloc((void **)&ctx->counters, 256 * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->counters, 0, 256 * sizeof(uint32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        sm_shutdown(ctx);
+        return SM_E_HIP;
+    }
+    *out = ctx;
+    return SM_OK;
+}
+
+void sm_shutdown(sm_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->buffers) (void)hipFree((void *)kv.first);
+    ctx->buffers.clear();
+    if (ctx->counters) (void)hipFree(ctx->counters);
+    for (auto &e : ctx->events)
+        if (e) (void)hipEventDestroy(e);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char *sm_last_error(sm_ctx *ctx) { return ctx ? ctx->error.c_str() : "no context"; }
+
+int sm_info(sm_ctx *ctx, char *buf, size_t cap) {
+    if (!ctx || !buf) return SM_E_ARG;
+    hipDeviceProp_t p;
+    HIP_TRY(ctx, hipGetDeviceProperties(&p, ctx->device));
+    int n = snprintf(buf, cap,
+                     "{\"backend\":\"hip\",\"device\":%d,\"name\":\"%s\",\"arch\":\"%s\",\"computeUnits\":%d,"
+                     "\"globalMemoryBytes\":%llu,\"dispatches\":%llu,\"allocatedBytes\":%llu,\"buffers\":%zu,"
+                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu}",
+                     ctx->device, p.name, p.gcnArchName, p.multiProcessorCount, (unsigned long long)p.totalGlobalMem,
+                     (unsigned long long)ctx->launches, (unsigned long long)ctx->allocated, ctx->buffers.size(),
+                     (unsigned long long)ctx->bytes_written, (unsigned long long)ctx->bytes_read);
+    return n;
+}
+
+int sm_alloc(sm_ctx *ctx, uint64_t bytes, int zero, uint64_t *handle) {
+    if (!ctx || !handle) return SM_E_ARG;
+    if (bytes == 0) return fail(ctx, SM_E_ARG, "allocation must be at least 1 byte");
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(ctx, SM_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    if (zero) {
+        e = hipMemsetAsync(p, 0, bytes, ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return hip_fail(ctx, e, "hipMemsetAsync");
+        }
+    }
+    ctx->buffers[(uint64_t)p] = bytes;
+    ctx->allocated += bytes;
+    *handle = (uint64_t)p;
+    return SM_OK;
+}
+
+int sm_free(sm_ctx *ctx, uint64_t handle) {
+    if (!ctx) return SM_E_ARG;
+    auto it = ctx->buffers.find(handle);
+    if (it == ctx->buffers.end()) return fail(ctx, SM_E_HANDLE, "free: not a live buffer of this context");
+    // Kernels already queued may still read the buffer.
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipFree((void *)handle));
+    ctx->allocated -= it->second;
+    ctx->buffers.erase(it);
+    return SM_OK;
+}
+
+int sm_size(sm_ctx *ctx, uint64_t handle, uint64_t *bytes) {
+    if (!ctx || !bytes) return SM_E_ARG;
+    auto it = ctx->buffers.find(handle);
+    if (it == ctx->buffers.end()) return fail(ctx, SM_E_HANDLE, "size: not a live buffer of this context");
+    *bytes = it->second;
+    return SM_OK;
+}
+
+int sm_write(sm_ctx *ctx, uint64_t dst, uint64_t dst_offset, const void *src, uint64_t bytes) {
+    if (!ctx || (!src && bytes)) return SM_E_ARG;
+    if (int rc = need(ctx, dst, dst_offset + bytes, "write")) return rc;
+    if (!bytes) return SM_OK;
+    HIP_TRY(ctx, hipMemcpyAsync((char *)dst + dst_offset, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->bytes_written += bytes;
+    return SM_OK;
+}
+
+int sm_read(sm_ctx *ctx, uint64_t src, uint64_t src_offset, void *dst, uint64_t bytes) {
+    if (!ctx || (!dst && bytes)) return SM_E_ARG;
+    if (int rc = need(ctx, src, src_offset + bytes, "read")) return rc;
+    if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, (const char *)src + src_offset, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->bytes_read += bytes;
+    return SM_OK;
+}
+
+int sm_copy(sm_ctx *ctx, uint64_t src, uint64_t src_offset, uint64_t dst, uint64_t dst_offset, uint64_t bytes) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = need(ctx, src, src_offset + bytes, "copy source")) return rc;
+    if (int rc = need(ctx, dst, dst_offset + bytes, "copy destination")) return rc;
+    if (bytes)
+        HIP_TRY(ctx, hipMemcpyAsync((char *)dst + dst_offset, (const char *)src + src_offset, bytes,
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+    return SM_OK;
+}
+
+int sm_zero(sm_ctx *ctx, uint64_t dst, uint64_t offset, uint64_t bytes) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = need(ctx, dst, offset + bytes, "zero")) return rc;
+    if (bytes) HIP_TRY(ctx, hipMemsetAsync((char *)dst + offset, 0, bytes, ctx->stream));
+    return SM_OK;
+}
+
+int sm_sync(sm_ctx *ctx) {
+    if (!ctx) return SM_E_ARG;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return SM_OK;
+}
+
+int sm_event_record(sm_ctx *ctx, int slot) {
+    if (!ctx || slot < 0 || slot >= 64) return SM_E_ARG;
+    HIP_TRY(ctx, hipEventRecord(ctx->events[slot], ctx->stream));
+    return SM_OK;
+}
+
+int sm_event_elapsed(sm_ctx *ctx, int a, int b, float *ms) {
+    if (!ctx || !ms || a < 0 || a >= 64 || b < 0 || b >= 64) return SM_E_ARG;
+    HIP_TRY(ctx, hipEventSynchronize(ctx->events[b]));
+    HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->events[a], ctx->events[b]));
+    return SM_OK;
+}
+
+// ------------------------------------------------------------- MoE layer
+static int check_geometry(sm_ctx *ctx, int tokens, int width, int ff, int experts, int topk) {
+    // src/model.js:14 and src/backend.js:12-13,29
+    if (tokens < 1 || width < 64 || ff < 64) return fail(ctx, SM_E_ARG, "tokens, width and ff must be positive");
+    if (width % 64 || ff % 64) return fail(ctx, SM_E_ARG, "Packed expert dimensions must contain complete groups");
+    if (experts < 1 || experts > 512 || topk < 1 || topk > (experts < 32 ? experts : 32))
+        return fail(ctx, SM_E_ARG, "Router supports 1-512 experts and topK <= min(experts,32)");
+    if ((int64_t)tokens * width > (int64_t)1 << 30 || (int64_t)tokens * topk > (int64_t)1 << 24)
+        return fail(ctx, SM_E_ARG, "token batch too large");
+    return SM_OK;
+}
+
+int sm_moe_route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t bias, int experts, int topk,
+                 uint64_t logits, uint64_t ids, uint64_t weights) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = check_geometry(ctx, tokens, width, 64, experts, topk)) return rc;
+    return route(ctx, X, tokens, width, Wr, bias, experts, topk, logits, ids, weights, 0, 0);
+}
+
+int sm_moe_dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets, uint64_t rows,
+                    uint64_t parts, uint64_t where_, uint64_t workspace, uint64_t workspace_bytes) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = check_geometry(ctx, tokens, 64, 64, experts, topk)) return rc;
+    return dispatch(ctx, ids, tokens, topk, experts, offsets, rows, parts, where_, workspace, workspace_bytes, 0);
+}
+
+int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes) {
+    if (!bytes || tokens < 1 || width < 64 || ff < 64 || width % 64 || ff % 64 || experts < 1 || experts > 512 ||
+        topk < 1 || topk > 32 || topk > experts)
+        return SM_E_ARG;
+    *bytes = tokens == 1 ? moe_decode_workspace(width, ff, experts, topk)
+                         : moe_prefill_workspace(tokens, width, ff, experts, topk);
+    return SM_OK;
+}
+
+int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
+                 uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y, uint64_t ids,
+                 uint64_t weights, uint64_t workspace, uint64_t workspace_bytes) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = check_geometry(ctx, tokens, width, ff, experts, topk)) return rc;
+    BlobLayout L = blob_layout(width, ff);
+    if (blob_stride < L.bytes || blob_stride % 256)
+        return fail(ctx, SM_E_ARG, "blob stride must be a multiple of 256 holding one blob");
+    if (int rc = need(ctx, arena, blob_stride * (uint64_t)(experts - 1) + L.bytes, "expert arena")) return rc;
+    if (int rc = need(ctx, shared_blob, L.bytes, "shared expert blob")) return rc;
+    if (int rc = need(ctx, X, (uint64_t)tokens * width * 4, "X")) return rc;
+    if (int rc = need(ctx, Y, (uint64_t)tokens * width * 4, "Y")) return rc;
+    if (int rc = need(ctx, Wr, (uint64_t)experts * width * 4, "router weights")) return rc;
+    if (int rc = need(ctx, Wsg, (uint64_t)width * 4, "shared gate weights")) return rc;
+    if (bias)
+        if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
+    if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
+    if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
+    uint64_t ws = tokens == 1 ? moe_decode_workspace(width, ff, experts, topk)
+                              : moe_prefill_workspace(tokens, width, ff, experts, topk);
+    if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
+    if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
+    if (tokens == 1)
+        return moe_decode(ctx, X, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
+                          weights, workspace, workspace_bytes);
+    return moe_prefill(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
+                       weights, workspace, workspace_bytes);
+}
+
+}  // extern "C"
