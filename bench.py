@@ -1,0 +1,309 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput on one MI355X.
+
+Workload (the single-layer decode configuration): one MoE layer, T=1 token
+per step, hidden 2048, 512 experts, top-10 + shared expert, Q2 experts
+(64-weight fp16-scale groups, 884,736-byte blobs), f32 activations,
+RMSNorm'd N(0,1) inputs. 48 independent layers (21.7 GB of expert blobs) stay
+resident in HBM and successive steps rotate through them, so a step never
+finds its weights in the 256 MB Infinity Cache. A step is one token through
+one layer: device routing, gate/up, down and combine, no host round trip.
+
+Timing: W untimed warm-up steps, then exactly K steps (K/48 replays of a HIP
+graph holding 48 steps, plus a partial graph if K is not a multiple of 48),
+bracketed by a device synchronisation on both sides; value = K / seconds.
+
+roofline: the dominant decode kernel's algorithmic bytes per launch divided by
+its average duration, from graphs that run only that stage (HIP events on the
+library's stream around the replays); peak = 8 TB/s HBM. traffic (HBM bytes
+per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated) is
+read from profiles/traffic.json when present.
+
+prefill: T=512 (uniform routing) and T=2048 (Zipf(1.1) router prior) through
+the grouped-MFMA path, per-stage times from events, reported beside the main
+line. cpu_baseline: the CPU oracle (a restatement of the reference kernels in
+their operation order, OpenMP over workgroups) on the host cores, T=1 decode
+of a bounded token sample of the same layer.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer tok/s (T=1 decode, T=512 prefill); % HBM GB/s / % MFMA roofline"
+PEAK_HBM = 8.0e12         # bytes/s, MI355X HBM3E
+PEAK_MFMA_F16 = 2.5e15    # dense fp16/bf16 MFMA FLOP/s
+
+
+def decode_kernel_bytes(W, F, E, K):
+    """Algorithmic bytes per launch of each decode kernel (weights streamed +
+    inputs read + outputs written; logits/hidden intermediates excluded)."""
+    gu_blob = 2 * F * W // 4 + 2 * F * (W // 64) * 2
+    dn_blob = W * F // 4 + W * (F // 64) * 2
+    return {
+        "decode_route": E * W * 4 + W * 4 + W * 4 + gu_blob + 4,   # W_r, w_sg, x, shared gate/up plane; gate
+        "decode_gate_up": K * gu_blob + W * 4 + K * 8,             # 10 routed gate/up planes, x; ids, weights
+        "decode_down_combine": (K + 1) * dn_blob + W * 4 + K * 8,  # 11 down planes; y; ids, weights
+    }
+
+
+def layer_bytes(W, F, E, K, T, distinct):
+    """Algorithmic bytes of one layer launch: distinct expert blobs touched +
+    shared blob + router and gate weights + inputs and outputs."""
+    blob = 2 * F * W // 4 + W * F // 4 + 2 * F * (W // 64) * 2 + W * (F // 64) * 2
+    return distinct * blob + blob + E * W * 4 + W * 4 + 2 * T * W * 4
+
+
+def layer_flops(W, F, E, K, T):
+    return T * ((K + 1) * 3 * 2 * W * F + 2 * E * W)
+
+
+def read_traffic(kernel):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        data = json.load(open(path))
+        return data.get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(oracle, wl, seconds):
+    import numpy as np
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    host = wl.host_layer(oracle, 0)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    n, t0 = 0, time.perf_counter()
+    ones = np.ones(W, np.float32)
+    while True:
+        z = oracle.synth_normal(W, host["seed"] + 5000 + n, wl.STREAM_INPUT, 1.0)
+        x = oracle.norm(z, ones, W, 1)
+        oracle.moe_layer(x, 1, host["Wr"], host["arena"], host["stride"], host["shared"], host["Wsg"], W, F, E, K)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 4096:
+            break
+    return {"value": n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": "%d single-token decodes of one full-geometry MoE layer (T=1), CPU oracle in the reference "
+                      "kernels' f32 operation order, OpenMP over workgroups, %.1f s" % (n, el)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4800)
+    ap.add_argument("--warmup", type=int, default=96)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only run the copy kernel used to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs the MoE layer on a single MI355X (no multi-GPU path); "
+              "use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0 or args.layers < 1:
+        sys.exit("steps >= 1, warmup >= 0, layers >= 1")
+
+    import numpy as np
+    import stratacuda_amd as sm
+    from stratacuda_amd import workload as wl
+
+    be = sm.Backend(0)
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+
+    if args.calibrate:
+        n = 64 * 1024 * 1024  # 256 MiB read + 256 MiB written per launch
+        a, b = be.alloc(n, zero=True), be.alloc(n)
+        for _ in range(5):
+            be.run("strata_elementwise", {"A": a, "B": a, "Y": b, "n": n, "mode": 0, "scale": 1.0}, [n // 64, 1, 1])
+        be.sync()
+        print(json.dumps({"calibration": "strata_elementwise copy", "bytes_read": n * 4, "bytes_written": n * 4}))
+        return
+
+    L = args.layers
+    print("bench: building %d resident layers (%.1f GB of expert blobs)" % (L, L * E * wl.blob_stride() / 1e9),
+          file=sys.stderr, flush=True)
+    layers = [wl.DeviceLayer(be, l) for l in range(L)]
+    ones = be.alloc(np.ones(W, np.float32))
+    slots = []
+    for i in range(L):
+        z = be.alloc(W, zero=False)
+        be.synth_normal(z, W, wl.layer_seed(i) + 99, wl.STREAM_INPUT, 1.0)
+        x = be.alloc(W, zero=False)
+        be.run("strata_norm", {"X": z, "W": ones, "Y": x, "cols": W, "rows": 1, "weightRows": 1, "mode": 0,
+                               "epsilon": 1e-6, "scale": 1.0}, [1, 1, 1])
+        slots.append({"x": x, "y": be.alloc(W), "ids": be.alloc(K, "i32"), "w": be.alloc(K),
+                      "ws": be.alloc_bytes(be.moe_workspace_bytes(1, W, F, E, K))})
+
+    def step(i):
+        s, lay = slots[i], layers[i]
+        be.moe_layer(s["x"], 1, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, s["y"], s["ids"],
+                     s["w"], s["ws"])
+
+    for s in range(args.warmup):
+        step(s % L)
+    be.sync()
+    for s in slots:
+        ids = be.read(s["ids"])
+        assert ids.min() >= 0 and ids.max() < E and len(set(ids)) == K
+        assert np.all(np.isfinite(be.read(s["y"])))
+
+    # ---- timed region: exactly K steps from graph replays
+    be.graph_begin()
+    for i in range(L):
+        step(i)
+    g_full = be.graph_end()
+    rem = args.steps % L
+    g_rem = None
+    if rem:
+        be.graph_begin()
+        for i in range(rem):
+            step(i)
+        g_rem = be.graph_end()
+    be.graph_launch(g_full)  # warm the graph itself
+    be.sync()
+    be.sync()
+    t0 = time.perf_counter()
+    be.event_record(0)
+    for _ in range(args.steps // L):
+        be.graph_launch(g_full)
+    if g_rem is not None:
+        be.graph_launch(g_rem)
+    be.event_record(1)
+    be.sync()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    gpu_ms = be.event_elapsed_ms(0, 1)
+    ms_per_step = wall * 1e3 / args.steps
+
+    # ---- per-kernel durations: graphs that run one decode stage each
+    kernel_bytes = decode_kernel_bytes(W, F, E, K)
+    kernels = {}
+    reps = max(1, min(50, 2400 // L))
+    for stage, name in enumerate(["decode_route", "decode_gate_up", "decode_down_combine"]):
+        be.stage_select(1 << stage)
+        be.graph_begin()
+        for i in range(L):
+            step(i)
+        gid = be.graph_end()
+        be.stage_select()
+        be.graph_launch(gid)
+        be.sync()
+        be.event_record(2)
+        for _ in range(reps):
+            be.graph_launch(gid)
+        be.event_record(3)
+        be.sync()
+        us = be.event_elapsed_ms(2, 3) * 1e3 / (reps * L)
+        gbs = kernel_bytes[name] / (us * 1e-6) / 1e9
+        kernels[name] = {"avg_us": round(us, 3), "bytes_per_launch": kernel_bytes[name], "GB/s": round(gbs, 1),
+                         "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4)}
+        be.graph_free(gid)
+    dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
+    hip_kernel = {"decode_route": "k_decode_route", "decode_gate_up": "k_decode_gate_up",
+                  "decode_down_combine": "k_decode_down"}[dom]
+    roofline = {"bound": "hbm", "kernel": hip_kernel, "achieved": kernels[dom]["GB/s"], "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": kernels[dom]["frac_hbm"], "traffic": read_traffic(hip_kernel),
+                "bytes_per_launch": kernels[dom]["bytes_per_launch"], "avg_us": kernels[dom]["avg_us"]}
+    # whole step (all three kernels), against the per-token algorithmic bytes
+    step_bytes = layer_bytes(W, F, E, K, 1, K)
+    step_s = gpu_ms * 1e-3 / args.steps
+    layer_roof = {"bound": "hbm", "bytes_per_step": step_bytes, "achieved": round(step_bytes / step_s / 1e9, 1),
+                  "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(step_bytes / step_s / PEAK_HBM, 4),
+                  "gpu_us_per_step": round(step_s * 1e6, 3)}
+
+    # ---- prefill (grouped MFMA path)
+    prefill = None
+    if not args.no_prefill:
+        prefill = {}
+        for T, zipf in ((512, False), (2048, True)):
+            Xs = []
+            for j in range(2):
+                X = be.alloc(T * W, zero=False)
+                be.synth_normal(X, T * W, wl.layer_seed(j) + 7 + T, wl.STREAM_INPUT, 1.0)
+                Xs.append(X)
+            bias = be.alloc(wl.zipf_bias(E, wl.layer_seed(0))) if zipf else None
+            Y, ids, w = be.alloc(T * W), be.alloc(T * K, "i32"), be.alloc(T * K)
+            ws = be.alloc_bytes(be.moe_workspace_bytes(T, W, F, E, K))
+
+            def run(j):
+                lay = layers[j % L]
+                be.moe_layer(Xs[j % 2], T, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, Y, ids,
+                             w, ws, bias=bias)
+
+            for j in range(3):
+                run(j)
+            be.sync()
+            be.stage_timing(True)
+            be.event_record(4)
+            for j in range(args.prefill_reps):
+                run(j)
+            be.event_record(5)
+            be.sync()
+            rep = be.stage_report()
+            be.stage_timing(False)
+            ms = be.event_elapsed_ms(4, 5) / args.prefill_reps
+            got = be.read(ids)
+            distinct = len(np.unique(got))
+            counts = np.sort(np.bincount(got, minlength=E))[::-1]
+            M = T * (K + 1)
+            stages = {k: round(v[0] / max(1, v[1]) * 1e3, 2) for k, v in rep.items() if v[1]}
+            gu_us, dn_us = stages.get("prefill_gate_up_gemm", 0.0), stages.get("prefill_down_gemm", 0.0)
+            gu_fl, dn_fl = 2.0 * M * 2 * F * W, 2.0 * M * W * F
+            lb = layer_bytes(W, F, E, K, T, distinct)
+            lf = layer_flops(W, F, E, K, T)
+            prefill["T=%d%s" % (T, " zipf" if zipf else "")] = {
+                "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_layer": round(ms, 4),
+                "distinct_experts": int(distinct), "top20_share": round(float(counts[:20].sum() / got.size), 3),
+                "stage_us": stages,
+                "hbm": {"bytes": lb, "achieved_GBs": round(lb / (ms * 1e-3) / 1e9, 1),
+                        "frac": round(lb / (ms * 1e-3) / PEAK_HBM, 4)},
+                "mfma": {"layer_flops": lf, "layer_frac": round(lf / (ms * 1e-3) / PEAK_MFMA_F16, 4),
+                         "gate_up_gemm_TFLOPs": round(gu_fl / (gu_us * 1e-6) / 1e12, 1) if gu_us else None,
+                         "gate_up_gemm_frac": round(gu_fl / (gu_us * 1e-6) / PEAK_MFMA_F16, 4) if gu_us else None,
+                         "down_gemm_frac": round(dn_fl / (dn_us * 1e-6) / PEAK_MFMA_F16, 4) if dn_us else None,
+                         "peak": "2.5 PFLOP/s dense fp16/bf16"},
+                "dtype": "f32 in/out; experts on fp16 MFMA (exact fp16 weights, activations split hi+lo), f32 accumulate",
+            }
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        cpu = cpu_baseline(oracle, wl, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(args.steps / wall, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded counter-based generator; random-init Q2 experts of the reference layout)",
+        "config": {"workload": "single MoE layer decode, T=1: hidden 2048, 512 experts, top-10 + shared, Q2 "
+                               "(64-weight fp16-scale groups), 48 resident layers rotated per step",
+                   "tokens_per_step": 1, "layers_rotated": L, "execution": "HIP graph of 48 steps",
+                   "gpu_us_per_step": round(gpu_ms * 1e3 / args.steps, 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "layer_roofline": layer_roof,
+        "kernels": kernels,
+        "prefill": prefill,
+    }
+    print(json.dumps(out))
+    be.dispose()
+
+
+if __name__ == "__main__":
+    main()

@@ -127,6 +127,31 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
 int sm_event_record(sm_ctx *ctx, int slot);          /* slot in [0, 64) */
 int sm_event_elapsed(sm_ctx *ctx, int start_slot, int end_slot, float *ms);
 
+/* Per-stage timing of sm_moe_layer (no reference counterpart; the reference
+ * exposes counters through GpuBackend.info, src/backend.js:120). When enabled,
+ * an event is recorded on the context's stream at every stage boundary;
+ * sm_stage_report synchronises and returns, per stage, the accumulated
+ * milliseconds and call counts since enabling (n >= 8 slots). Stages:
+ * 0 decode route, 1 decode gate/up, 2 decode down+combine, 3 prefill route
+ * (router GEMM + top-k), 4 prefill dispatch, 5 prefill gate/up GEMM,
+ * 6 prefill down GEMM, 7 prefill combine. Returns the number of stages. */
+int sm_stage_timing(sm_ctx *ctx, int enable);
+int sm_stage_report(sm_ctx *ctx, double *total_ms, uint64_t *calls, int n);
+/* Runs only the sm_moe_layer stages whose bit (1 << stage) is set; the
+ * default is all. A profiling aid: the caller must already have run the
+ * skipped stages on the same workspace, ids and weights. */
+int sm_stage_select(sm_ctx *ctx, uint32_t mask);
+
+/* HIP graphs of launch sequences (no reference counterpart; the reference
+ * batches up to 128 dispatches per WebGPU submit, src/backend.js:76-83).
+ * Between sm_graph_begin and sm_graph_end, launches on the context are
+ * captured instead of run; calls that synchronise (read, write, free, sync,
+ * index validation of reference kernels) fail while capturing. */
+int sm_graph_begin(sm_ctx *ctx);
+int sm_graph_end(sm_ctx *ctx, int *graph_id);
+int sm_graph_launch(sm_ctx *ctx, int graph_id);
+int sm_graph_free(sm_ctx *ctx, int graph_id);
+
 /* ------------------------------------------------------ synthetic inputs */
 /* No reference counterpart. Deterministic seeded data, bit-identical to the
  * CPU oracle's generator:

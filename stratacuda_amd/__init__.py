@@ -66,6 +66,13 @@ def lib():
             "sm_moe_dispatch": (i, [vp, u64, i, i, i, u64, u64, u64, u64, u64, u64]),
             "sm_moe_layer_workspace": (i, [i, i, i, i, i, pu64]),
             "sm_moe_layer": (i, [vp, u64, i, u64, u64, u64, u64, u64, u64, i, i, i, i, u64, u64, u64, u64, u64]),
+            "sm_stage_timing": (i, [vp, i]),
+            "sm_stage_report": (i, [vp, ctypes.POINTER(ctypes.c_double), pu64, i]),
+            "sm_stage_select": (i, [vp, ctypes.c_uint32]),
+            "sm_graph_begin": (i, [vp]),
+            "sm_graph_end": (i, [vp, ctypes.POINTER(i)]),
+            "sm_graph_launch": (i, [vp, i]),
+            "sm_graph_free": (i, [vp, i]),
             "sm_event_record": (i, [vp, i]),
             "sm_event_elapsed": (i, [vp, i, i, ctypes.POINTER(ctypes.c_float)]),
             "sm_synth_normal": (i, [vp, u64, u64, u64, u64, u64, ctypes.c_double]),
@@ -275,6 +282,38 @@ class Backend:
                                        workspace.nbytes))
 
     # ------------------------------------------------------------ timing
+    STAGES = ["decode_route", "decode_gate_up", "decode_down_combine", "prefill_route", "prefill_dispatch",
+              "prefill_gate_up_gemm", "prefill_down_gemm", "prefill_combine"]
+
+    def stage_timing(self, enable=True):
+        self._check(lib().sm_stage_timing(self._ctx, 1 if enable else 0))
+
+    def stage_report(self):
+        """{stage: (total_ms, calls)} accumulated since stage_timing(True)."""
+        ms = (ctypes.c_double * 16)()
+        calls = (ctypes.c_uint64 * 16)()
+        n = lib().sm_stage_report(self._ctx, ms, calls, 16)
+        if n < 0:
+            self._check(n)
+        return {self.STAGES[k]: (ms[k], calls[k]) for k in range(n)}
+
+    def stage_select(self, mask=0xffffffff):
+        self._check(lib().sm_stage_select(self._ctx, mask))
+
+    def graph_begin(self):
+        self._check(lib().sm_graph_begin(self._ctx))
+
+    def graph_end(self):
+        gid = ctypes.c_int()
+        self._check(lib().sm_graph_end(self._ctx, ctypes.byref(gid)))
+        return gid.value
+
+    def graph_launch(self, gid):
+        self._check(lib().sm_graph_launch(self._ctx, gid))
+
+    def graph_free(self, gid):
+        self._check(lib().sm_graph_free(self._ctx, gid))
+
     def event_record(self, slot):
         self._check(lib().sm_event_record(self._ctx, slot))
 

@@ -5,6 +5,7 @@
 
 #include <map>
 #include <string>
+#include <vector>
 
 #include "../../include/strata_mi355x.h"
 
@@ -18,6 +19,23 @@ struct sm_ctx {
     // (route completion counters). Each kernel returns its counter to zero.
     uint32_t *counters = nullptr;
     uint64_t launches = 0, bytes_written = 0, bytes_read = 0, allocated = 0;
+    // Stage timing (sm_stage_timing): events recorded at stage boundaries.
+    bool stage_timing = false;
+    std::vector<hipEvent_t> stage_pool;
+    size_t stage_used = 0;
+    struct Mark {
+        int stage;       // stage that starts at this event, -1 = end of a call
+        size_t event;    // index into stage_pool
+    };
+    std::vector<Mark> marks;
+    double stage_ms[16] = {};
+    uint64_t stage_calls[16] = {};
+    // Stages sm_moe_layer runs (bit per Stage); all by default. A caller that
+    // clears bits must have run the skipped stages on the same workspace.
+    uint32_t stage_mask = 0xffffffffu;
+    // Instantiated HIP graphs (sm_graph_*); nullptr marks a freed slot.
+    std::vector<hipGraphExec_t> graphs;
+    bool capturing = false;
 };
 
 namespace smi {
@@ -29,6 +47,24 @@ int need(sm_ctx *ctx, uint64_t handle, uint64_t bytes, const char *what);
 int launched(sm_ctx *ctx);  // checks hipGetLastError after a launch
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Stage boundaries for sm_stage_timing: stage_mark(ctx, s) records the start
+// of stage s (ending the previous one); stage_mark(ctx, -1) ends the call.
+enum Stage {
+    kStageDecodeRoute = 0,
+    kStageDecodeGateUp = 1,
+    kStageDecodeDown = 2,
+    kStagePrefillRoute = 3,
+    kStagePrefillDispatch = 4,
+    kStagePrefillGateUp = 5,
+    kStagePrefillDown = 6,
+    kStagePrefillCombine = 7,
+    kStageCount = 8
+};
+int stage_mark(sm_ctx *ctx, int stage);
+inline bool stage_on(const sm_ctx *ctx, int stage) { return (ctx->stage_mask >> stage) & 1u; }
+// Zero-fills n 32-bit words with a kernel (graph-capturable, unlike a memset node).
+int zero_words(sm_ctx *ctx, void *dst, uint64_t n);
 
 // Launchers defined in the kernel translation units.
 int route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t bias, int experts, int topk,

@@ -257,6 +257,7 @@ int64_t buf_len(sm_ctx *ctx, uint64_t h) {
 int check_indices(sm_ctx *ctx, uint64_t buf, int64_t n, int64_t stride, int64_t first, int lo, int hi,
                   const char *what) {
     if (n <= 0) return SM_OK;
+    if (ctx->capturing) return fail(ctx, SM_E_ARG, std::string(what) + ": index validation is not allowed while capturing");
     uint32_t *bad_flag = ctx->counters + 255;
     hipError_t e = hipMemsetAsync(bad_flag, 0, 4, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipMemsetAsync");

@@ -233,33 +233,39 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     BlobLayout L = blob_layout(width, ff);
     if ((2 * ff) % NB || width % NB)
         return fail(ctx, SM_E_ARG, "prefill needs width and 2*ff to be multiples of 128");
+    if (int rc = stage_mark(ctx, kStagePrefillRoute)) return rc;
     if (int rc = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts,
                               topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
                               (float *)(ws + w.gate)))
         return rc;
     int *offsets = (int *)(ws + w.offsets), *tile_base = (int *)(ws + w.tile_base);
+    if (int rc = stage_mark(ctx, kStagePrefillDispatch)) return rc;
     if (int rc = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
                                  (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, tile_base))
         return rc;
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const unsigned max_tiles = (unsigned)(m / MT + (uint64_t)experts + 2);
     dim3 g1((unsigned)(2 * ff / NB), max_tiles);
+    if (int rc = stage_mark(ctx, kStagePrefillGateUp)) return rc;
     k_grouped_gemm<true><<<g1, 256, 0, ctx->stream>>>((const float *)X, (const int *)(ws + w.rows), offsets, tile_base,
                                                       (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob,
                                                       experts, L.gate_up_codes, L.gate_up_scales, width, 2 * ff,
                                                       (float *)(ws + w.H), ff);
     if (int rc = launched(ctx)) return rc;
     dim3 g2((unsigned)(width / NB), max_tiles);
+    if (int rc = stage_mark(ctx, kStagePrefillDown)) return rc;
     k_grouped_gemm<false><<<g2, 256, 0, ctx->stream>>>((const float *)(ws + w.H), nullptr, offsets, tile_base,
                                                        (const uint8_t *)arena, blob_stride,
                                                        (const uint8_t *)shared_blob, experts, L.down_codes,
                                                        L.down_scales, ff, width, (float *)(ws + w.P), width);
     if (int rc = launched(ctx)) return rc;
     const uint64_t total = (uint64_t)tokens * width;
+    if (int rc = stage_mark(ctx, kStagePrefillCombine)) return rc;
     k_combine<<<(unsigned)((total + 255) / 256), 256, 0, ctx->stream>>>(
         (const float *)(ws + w.P), (const int *)(ws + w.where_), (const float *)weights, (const float *)(ws + w.gate),
         offsets, (float *)Y, tokens, topk, width, experts);
-    return launched(ctx);
+    if (int rc = launched(ctx)) return rc;
+    return stage_mark(ctx, -1);
 }
 
 }  // namespace smi

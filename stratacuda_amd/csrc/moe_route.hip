@@ -5,8 +5,10 @@
 // the tree s = 32..1), so selected expert IDs and their order are bit-exact
 // with the reference's CPU path; the top-k is router_wave (strata.cu:240-270).
 //
-//  * tokens == 1: one wave per router row; the last wave to finish (elected
-//    with a device-scope counter) runs the top-k, so routing is one launch.
+//  * tokens == 1: one wave per router row (all of a lane's loads issued
+//    before its sequential sum), then a one-wave top-k kernel. The kernel
+//    boundary orders the two; a per-block completion counter with device-
+//    scope fences measured an order of magnitude slower on MI355X.
 //  * tokens > 1: register-tiled exact GEMM. Each wave owns 8 tokens x 8 rows
 //    and keeps, per lane l, the 64 partial sums of "lane l" of the reference
 //    workgroup for all 64 outputs. A transpose (butterfly) reduction then
@@ -31,41 +33,33 @@ using namespace smi;
 namespace {
 
 // ------------------------------------------------------------ T = 1 route
-// Rows [0, experts) are router rows, row `experts` is the shared-expert gate
-// (when gate_w != 0). One 64-thread block per row.
-__global__ void __launch_bounds__(64) k_route_t1(const float *__restrict__ X, const float *__restrict__ Wr,
-                                                 const float *__restrict__ bias, const float *__restrict__ Wsg,
-                                                 float *__restrict__ logits, float *__restrict__ gate_out,
-                                                 int *__restrict__ ids, float *__restrict__ weights, int width,
-                                                 int experts, int topk, uint32_t *counter, int total_rows) {
+// One 64-thread block per row: rows [0, experts) are router rows, row
+// `experts` is the shared-expert gate (when gate_w != 0). NJ = width / 64
+// loads per lane, all issued before the (sequential, reference-order) sum.
+template <int NJ>
+__global__ void __launch_bounds__(64) k_route_rows(const float *__restrict__ X, const float *__restrict__ Wr,
+                                                   const float *__restrict__ bias, const float *__restrict__ Wsg,
+                                                   float *__restrict__ logits, float *__restrict__ gate_out, int width,
+                                                   int experts) {
     const int row = blockIdx.x, lane = threadIdx.x;
     const float *w = row < experts ? Wr + (int64_t)row * width : Wsg;
     float sum = 0.0f;
-    int i = lane;
-    // 4 independent loads in flight per iteration; the sum stays sequential.
-    for (; i + 192 < width; i += 256) {
-        float w0 = w[i], w1 = w[i + 64], w2 = w[i + 128], w3 = w[i + 192];
-        float x0 = X[i], x1 = X[i + 64], x2 = X[i + 128], x3 = X[i + 192];
-        sum = sum + w0 * x0;
-        sum = sum + w1 * x1;
-        sum = sum + w2 * x2;
-        sum = sum + w3 * x3;
+    if (NJ > 0) {
+        float wv[NJ > 0 ? NJ : 1], xv[NJ > 0 ? NJ : 1];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) wv[j] = __builtin_nontemporal_load(w + lane + 64 * j);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) xv[j] = X[lane + 64 * j];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) sum = sum + wv[j] * xv[j];
+    } else {
+        for (int i = lane; i < width; i += 64) sum = sum + w[i] * X[i];
     }
-    for (; i < width; i += 64) sum = sum + w[i] * X[i];
     sum = sm::tree_sum64(sum);
     if (lane == 0) {
         if (row < experts) logits[row] = bias ? sum + bias[row] : sum;
         else gate_out[0] = sum;
     }
-    // Elect the last row to finish; it runs the top-k over all logits.
-    __threadfence();
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0, 64);
-    if (old != (uint32_t)total_rows - 1) return;
-    __threadfence();
-    sm::router_wave(logits, ids, weights, experts, topk);
-    if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // -------------------------------------------------------- T > 1 route GEMM
@@ -136,9 +130,13 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
 
 __global__ void __launch_bounds__(256) k_topk(const float *__restrict__ logits, int *__restrict__ ids,
                                               float *__restrict__ weights, int tokens, int experts, int topk) {
+    __shared__ uint64_t s_tab[32];
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = sm::kExp2Tab[threadIdx.x];
+    __syncthreads();
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;
-    sm::router_wave(logits + (int64_t)t * experts, ids + (int64_t)t * topk, weights + (int64_t)t * topk, experts, topk);
+    sm::router_wave(logits + (int64_t)t * experts, ids + (int64_t)t * topk, weights + (int64_t)t * topk, experts, topk,
+                    s_tab);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -276,8 +274,12 @@ int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float
                  int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out) {
     if (tokens == 1) {
         const int total = experts + (gate_w ? 1 : 0);
-        k_route_t1<<<total, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, ids, weights, width, experts,
-                                                  topk, ctx->counters + 0, total);
+        if (width == 2048)
+            k_route_rows<32><<<total, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts);
+        else
+            k_route_rows<0><<<total, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts);
+        if (int rc = launched(ctx)) return rc;
+        k_topk<<<1, 64, 0, ctx->stream>>>(logits, ids, weights, 1, experts, topk);
         return launched(ctx);
     }
     const int nrows = experts + (gate_w ? 1 : 0);
@@ -323,8 +325,7 @@ int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int exper
     const int nb = ceil_div(tokens, 64);
     DispatchWs w = dispatch_ws(tokens, experts);
     const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
-    hipError_t e = hipMemsetAsync(ws + w.status, 0, 64, ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "hipMemsetAsync");
+    if (int rc = zero_words(ctx, ws + w.status, 16)) return rc;
     k_dispatch_masks<<<nb, 256, 0, ctx->stream>>>(ids, tokens, topk, experts, nb, (unsigned long long *)(ws + w.masks),
                                                   (int *)(ws + w.counts), (uint32_t *)(ws + w.status));
     if (int rc = launched(ctx)) return rc;

@@ -37,6 +37,39 @@ int launched(sm_ctx *ctx) {
     return SM_OK;
 }
 
+// Folds recorded stage events into the per-stage totals (synchronises).
+static int stage_fold(sm_ctx *ctx) {
+    if (ctx->marks.empty()) return SM_OK;
+    hipError_t e = hipEventSynchronize(ctx->stage_pool[ctx->marks.back().event]);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipEventSynchronize");
+    for (size_t i = 0; i + 1 < ctx->marks.size(); i++) {
+        const auto &a = ctx->marks[i], &b = ctx->marks[i + 1];
+        if (a.stage < 0) continue;
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, ctx->stage_pool[a.event], ctx->stage_pool[b.event]);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipEventElapsedTime");
+        ctx->stage_ms[a.stage] += ms;
+        ctx->stage_calls[a.stage] += 1;
+    }
+    ctx->marks.clear();
+    ctx->stage_used = 0;
+    return SM_OK;
+}
+
+int stage_mark(sm_ctx *ctx, int stage) {
+    if (!ctx->stage_timing) return SM_OK;
+    if (ctx->stage_used == ctx->stage_pool.size()) {
+        // Pool exhausted: fold at a call boundary only (a mark of -1 ends a call).
+        if (int rc = stage_fold(ctx)) return rc;
+    }
+    size_t idx = ctx->stage_used++;
+    hipError_t e = hipEventRecord(ctx->stage_pool[idx], ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipEventRecord");
+    ctx->marks.push_back({stage, idx});
+    if (stage < 0 && ctx->stage_used + 16 > ctx->stage_pool.size()) return stage_fold(ctx);
+    return SM_OK;
+}
+
 }  // namespace smi
 
 using namespace smi;
@@ -83,6 +116,9 @@ void sm_shutdown(sm_ctx *ctx) {
     for (auto &kv : ctx->buffers) (void)hipFree((void *)kv.first);
     ctx->buffers.clear();
     if (ctx->counters) (void)hipFree(ctx->counters);
+    for (auto &e : ctx->stage_pool) (void)hipEventDestroy(e);
+    for (auto &g : ctx->graphs)
+        if (g) (void)hipGraphExecDestroy(g);
     for (auto &e : ctx->events)
         if (e) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -125,6 +161,7 @@ int sm_alloc(sm_ctx *ctx, uint64_t bytes, int zero, uint64_t *handle) {
 }
 
 int sm_free(sm_ctx *ctx, uint64_t handle) {
+    if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     if (!ctx) return SM_E_ARG;
     auto it = ctx->buffers.find(handle);
     if (it == ctx->buffers.end()) return fail(ctx, SM_E_HANDLE, "free: not a live buffer of this context");
@@ -145,6 +182,7 @@ int sm_size(sm_ctx *ctx, uint64_t handle, uint64_t *bytes) {
 }
 
 int sm_write(sm_ctx *ctx, uint64_t dst, uint64_t dst_offset, const void *src, uint64_t bytes) {
+    if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     if (!ctx || (!src && bytes)) return SM_E_ARG;
     if (int rc = need(ctx, dst, dst_offset + bytes, "write")) return rc;
     if (!bytes) return SM_OK;
@@ -155,6 +193,7 @@ int sm_write(sm_ctx *ctx, uint64_t dst, uint64_t dst_offset, const void *src, ui
 }
 
 int sm_read(sm_ctx *ctx, uint64_t src, uint64_t src_offset, void *dst, uint64_t bytes) {
+    if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     if (!ctx || (!dst && bytes)) return SM_E_ARG;
     if (int rc = need(ctx, src, src_offset + bytes, "read")) return rc;
     if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, (const char *)src + src_offset, bytes, hipMemcpyDeviceToHost, ctx->stream));
@@ -181,8 +220,80 @@ int sm_zero(sm_ctx *ctx, uint64_t dst, uint64_t offset, uint64_t bytes) {
 }
 
 int sm_sync(sm_ctx *ctx) {
+    if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     if (!ctx) return SM_E_ARG;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return SM_OK;
+}
+
+int sm_stage_timing(sm_ctx *ctx, int enable) {
+    if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
+    if (!ctx) return SM_E_ARG;
+    if (int rc = stage_fold(ctx)) return rc;
+    for (int i = 0; i < kStageCount; i++) {
+        ctx->stage_ms[i] = 0.0;
+        ctx->stage_calls[i] = 0;
+    }
+    if (enable && ctx->stage_pool.empty()) {
+        ctx->stage_pool.resize(4096);
+        for (auto &e : ctx->stage_pool) HIP_TRY(ctx, hipEventCreate(&e));
+    }
+    ctx->stage_timing = enable != 0;
+    return SM_OK;
+}
+
+int sm_stage_report(sm_ctx *ctx, double *total_ms, uint64_t *calls, int n) {
+    if (!ctx || !total_ms || !calls || n < kStageCount) return SM_E_ARG;
+    if (int rc = stage_fold(ctx)) return rc;
+    for (int i = 0; i < kStageCount; i++) {
+        total_ms[i] = ctx->stage_ms[i];
+        calls[i] = ctx->stage_calls[i];
+    }
+    return kStageCount;
+}
+
+int sm_stage_select(sm_ctx *ctx, uint32_t mask) {
+    if (!ctx) return SM_E_ARG;
+    ctx->stage_mask = mask;
+    return SM_OK;
+}
+
+int sm_graph_begin(sm_ctx *ctx) {
+    if (!ctx) return SM_E_ARG;
+    if (ctx->capturing) return fail(ctx, SM_E_ARG, "a capture is already open");
+    if (ctx->stage_timing) return fail(ctx, SM_E_ARG, "disable stage timing before capturing a graph");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+    ctx->capturing = true;
+    return SM_OK;
+}
+
+int sm_graph_end(sm_ctx *ctx, int *graph_id) {
+    if (!ctx || !graph_id) return SM_E_ARG;
+    if (!ctx->capturing) return fail(ctx, SM_E_ARG, "no capture is open");
+    ctx->capturing = false;
+    hipGraph_t graph = nullptr;
+    HIP_TRY(ctx, hipStreamEndCapture(ctx->stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
+    ctx->graphs.push_back(exec);
+    *graph_id = (int)ctx->graphs.size() - 1;
+    return SM_OK;
+}
+
+int sm_graph_launch(sm_ctx *ctx, int graph_id) {
+    if (!ctx || graph_id < 0 || graph_id >= (int)ctx->graphs.size() || !ctx->graphs[graph_id]) return SM_E_ARG;
+    HIP_TRY(ctx, hipGraphLaunch(ctx->graphs[graph_id], ctx->stream));
+    return SM_OK;
+}
+
+int sm_graph_free(sm_ctx *ctx, int graph_id) {
+    if (!ctx || graph_id < 0 || graph_id >= (int)ctx->graphs.size() || !ctx->graphs[graph_id]) return SM_E_ARG;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipGraphExecDestroy(ctx->graphs[graph_id]));
+    ctx->graphs[graph_id] = nullptr;
     return SM_OK;
 }
 

@@ -44,7 +44,9 @@ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
-__device__ __forceinline__ float expf_or(float x) {
+// `tab` may point at a copy of kExp2Tab in LDS (a per-lane indexed load from
+// __constant__ memory goes through the vector memory path).
+__device__ __forceinline__ float expf_or(float x, const uint64_t *tab = kExp2Tab) {
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
@@ -64,7 +66,7 @@ __device__ __forceinline__ float expf_or(float x) {
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd = kd - Shift;
     double r = z - kd;
-    uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    uint64_t t = tab[ki % 32] + (ki << 47);
     double s = __longlong_as_double((long long)t);
     double zz = C0 * r + C1;
     double r2 = r * r;
@@ -74,27 +76,88 @@ __device__ __forceinline__ float expf_or(float x) {
     return (float)y;
 }
 // kernels/strata.cu:7-8
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf_or(-x)); }
-__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
+__device__ __forceinline__ float sigmoid(float x, const uint64_t *tab = kExp2Tab) {
+    return 1.0f / (1.0f + expf_or(-x, tab));
+}
+__device__ __forceinline__ float silu(float x, const uint64_t *tab = kExp2Tab) { return x * sigmoid(x, tab); }
 
 // --------------------------------------------------------- wave reductions
+// Cross-lane moves use DPP where the pattern allows: a DPP move costs a few
+// cycles, while a ds_bpermute shuffle (__shfl*) costs ~55 ns of latency on
+// MI355X. DPP controls (GFX9 encoding):
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- lane 7-i within 8
+constexpr int kDppRowMirror = 0x140;    // lane i <- lane 15-i within 16
+constexpr int kDppRowBcast15 = 0x142;   // row r+1 <- lane 15 of row r
+constexpr int kDppRowBcast31 = 0x143;   // rows 2,3 <- lane 31
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f32(float old, float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf,
+                                                                 false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i32(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
 // Tree sum over the 64 lanes in the reference order (s = 32, 16, ..., 1: lane
-// l adds lane l+s). The returned value is valid in lane 0.
+// l adds lane l+s), so the result is bit-identical to the reference's
+// shared-memory tree. Valid in lane 0. Levels 8..1 stay inside a 16-lane row
+// (DPP row_shl: lane i receives lane i+s); levels 32 and 16 cross rows.
 __device__ __forceinline__ float tree_sum64(float v) {
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) v = v + __shfl_down(v, s, 64);
+    v = v + __shfl_down(v, 32, 64);
+    v = v + __shfl_down(v, 16, 64);
+    v = v + dpp_f32<0x108>(0.0f, v);
+    v = v + dpp_f32<0x104>(0.0f, v);
+    v = v + dpp_f32<0x102>(0.0f, v);
+    v = v + dpp_f32<0x101>(0.0f, v);
     return v;
 }
-__device__ __forceinline__ float tree_max64(float v) {
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_down(v, s, 64));
+// Maximum over the 64 lanes (order-free), returned in every lane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v, v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v, v));
+    v = fmaxf(v, dpp_f32<kDppRowHalfMirror>(v, v));
+    v = fmaxf(v, dpp_f32<kDppRowMirror>(v, v));
+    v = fmaxf(v, dpp_f32<kDppRowBcast15, 0xa>(v, v));
+    v = fmaxf(v, dpp_f32<kDppRowBcast31, 0xc>(v, v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, dpp_i32<kDppQuadXor1>(v, v));
+    v = min(v, dpp_i32<kDppQuadXor2>(v, v));
+    v = min(v, dpp_i32<kDppRowHalfMirror>(v, v));
+    v = min(v, dpp_i32<kDppRowMirror>(v, v));
+    v = min(v, dpp_i32<kDppRowBcast15, 0xa>(v, v));
+    v = min(v, dpp_i32<kDppRowBcast31, 0xc>(v, v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, dpp_i32<kDppQuadXor1>(v, v));
+    v = max(v, dpp_i32<kDppQuadXor2>(v, v));
+    v = max(v, dpp_i32<kDppRowHalfMirror>(v, v));
+    v = max(v, dpp_i32<kDppRowMirror>(v, v));
+    v = max(v, dpp_i32<kDppRowBcast15, 0xa>(v, v));
+    v = max(v, dpp_i32<kDppRowBcast31, 0xc>(v, v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+// Sum within each group of 8 consecutive lanes (any order), in every lane.
+__device__ __forceinline__ float group8_sum(float v) {
+    v = v + dpp_f32<kDppQuadXor1>(0.0f, v);
+    v = v + dpp_f32<kDppQuadXor2>(0.0f, v);
+    v = v + dpp_f32<kDppRowHalfMirror>(0.0f, v);
     return v;
 }
-// Sum over groups of `width` consecutive lanes (valid in the group's first lane).
-template <int WIDTH>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int s = WIDTH / 2; s > 0; s >>= 1) v += __shfl_down(v, s, 64);
+// Sum within each 32-lane half (any order): valid in lanes 31 and 63.
+__device__ __forceinline__ float half32_sum(float v) {
+    v = v + dpp_f32<kDppQuadXor1>(0.0f, v);
+    v = v + dpp_f32<kDppQuadXor2>(0.0f, v);
+    v = v + dpp_f32<kDppRowHalfMirror>(0.0f, v);
+    v = v + dpp_f32<kDppRowMirror>(0.0f, v);
+    v = v + dpp_f32<kDppRowBcast15, 0xa>(0.0f, v);
     return v;
 }
 
@@ -141,10 +204,73 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return (uint16_t)(sign | half);
 }
 
-// kernels/strata.cu:240-270 strata_router / :479-509 strata_router_batch, one
-// 64-lane wave per token. Probabilities live in registers: lane l holds the
-// experts l, l+64, ... (at most 8 of them for 512 experts).
-__device__ __forceinline__ void router_wave(const float *Logits, int *Ids, float *Weights, int experts, int topK) {
+// Selection keys for the reference's top-k rounds (kernels/strata.cu:252-265).
+// A probability p >= +0 is keyed by its bit pattern read as int, which orders
+// exactly like the value; a selected expert holds -1.0f (kPickedKey, negative
+// as int, still above every key below); an expert past `experts` or with a NaN
+// probability gets INT_MIN, which the reference's `>` / `==` tests never pick.
+// kNoKey sits between the two: it is a lane's starting best, so a lane picks
+// the first selected (-1.0f) entry when nothing larger is left, as the
+// reference does, and keeps kNoKey (ID = experts) when it has no entry at all.
+constexpr int kPickedKey = (int)0xBF800000u;
+constexpr int kNoKey = kPickedKey - 1;
+__device__ __forceinline__ int select_key(float p, bool valid) {
+    return valid && p == p ? __builtin_bit_cast(int, p) : (int)0x80000000u;
+}
+// topK selection rounds over one wave; lane l holds the keys of experts
+// l + 64 j. Each round: every lane's best (first j among equal keys, i.e.
+// the lower ID), the wave maximum, and among lanes tied at the maximum the
+// lowest ID; that expert's key becomes kPickedKey. Lane 0 writes Ids[k];
+// lane k returns the selected probability of round k in `mine`.
+__device__ __forceinline__ void select_rounds(int (&key)[8], int experts, int topK, int *Ids, float &mine) {
+    const int lane = threadIdx.x & 63;
+    mine = 0.0f;
+    for (int k = 0; k < topK; ++k) {
+        int best = kNoKey, bj = 8;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const bool gt = key[j] > best;
+            best = gt ? key[j] : best;
+            bj = gt ? j : bj;
+        }
+        const int top = wave_max_i32(best);
+        int winner = experts;
+        if (top != kNoKey) {
+            const unsigned long long tied = __ballot(best == top);
+            const int id = lane + 64 * bj;
+            if (__popcll(tied) == 1) winner = __builtin_amdgcn_readlane(id, __ffsll((long long)tied) - 1);
+            else winner = wave_min_i32(best == top ? id : 0x7fffffff);
+        }
+        if (lane == 0) Ids[k] = winner;
+        if (lane == k) mine = top == kNoKey ? -1.0f : __builtin_bit_cast(float, top);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (winner == lane + 64 * j) key[j] = kPickedKey;
+    }
+}
+// kernels/strata.cu:266-269: weights = selected / max(sum(selected), 2^-14),
+// the sum taken sequentially over k. Lane k holds selected[k].
+__device__ __forceinline__ void router_weights(float mine, int topK, float *Weights) {
+    const int lane = threadIdx.x & 63;
+    float denom = 0.0f;
+    for (int k = 0; k < topK; ++k)
+        denom = denom + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), k));
+    denom = fmaxf(denom, 0.00006103515625f);
+    if (lane < topK) Weights[lane] = mine / denom;
+}
+
+// kernels/strata.cu:240-270 strata_router / :479-509 strata_router_batch for
+// one token, by one 64-lane wave, with the reference's results bit for bit:
+// probabilities follow the reference's operation order (lane-strided
+// sequential sums, then the reference tree), lane l holds experts l, l+64, ...
+// (at most 8 for 512 experts), and each of the topK rounds takes every lane's
+// best (the reference's lane loop, including its handling of already
+// selected experts) and the wave maximum; ties in probability go to the
+// lower expert ID, so the winner of a round is the same expert the
+// reference's tree reduction finds. The wave maximum uses DPP and a ballot
+// instead of a shuffle tree.
+__device__ __forceinline__ void router_wave(const float *Logits, int *Ids, float *Weights, int experts, int topK,
+                                            const uint64_t *tab = kExp2Tab) {
     const int lane = threadIdx.x & 63;
     float p[8];
     float mx = -3.402823e38f;
@@ -153,53 +279,68 @@ __device__ __forceinline__ void router_wave(const float *Logits, int *Ids, float
         int e = lane + 64 * j;
         if (e < experts) mx = fmaxf(mx, Logits[e]);
     }
-    mx = __shfl(sm::tree_max64(mx), 0, 64);
+    mx = wave_max(mx);
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         int e = lane + 64 * j;
         p[j] = 0.0f;
         if (e < experts) {
-            p[j] = sm::expf_or(Logits[e] - mx);
+            p[j] = expf_or(Logits[e] - mx, tab);
             sum = sum + p[j];
         }
     }
-    float inv = 1.0f / __shfl(sm::tree_sum64(sum), 0, 64);
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tree_sum64(sum))));
+    const float inv = 1.0f / sum;
+    int key[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) p[j] = p[j] * inv;
-    float mine = 0.0f;  // lane k keeps selected[k]
-    for (int k = 0; k < topK; ++k) {
-        float best = -1.0f;
-        int id = experts;
+    for (int j = 0; j < 8; j++) key[j] = select_key(p[j] * inv, lane + 64 * j < experts);
+    float mine;
+    select_rounds(key, experts, topK, Ids, mine);
+    router_weights(mine, topK, Weights);
+}
+
+// The same routing for one token by a 256-thread block: the 512 exponentials
+// are spread over all threads (table in LDS), wave 0 forms the reference sum
+// and runs the selection rounds. Results land in s_ids / s_w (LDS). Needs
+// blockDim.x == 256 and experts <= 512. s_tab must already hold kExp2Tab.
+struct RouterScratch {
+    float p[512];
+    float red[4];
+};
+__device__ __forceinline__ void router_block(const float *Logits, int experts, int topK, const uint64_t *s_tab,
+                                             RouterScratch &s, int *s_ids, float *s_w) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e0 = tid, e1 = tid + 256;
+    const float l0 = e0 < experts ? Logits[e0] : -3.402823e38f;
+    const float l1 = e1 < experts ? Logits[e1] : -3.402823e38f;
+    float mx = wave_max(fmaxf(l0, l1));
+    if (lane == 0) s.red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s.red[0], s.red[1]), fmaxf(s.red[2], s.red[3]));
+    if (e0 < experts) s.p[e0] = expf_or(l0 - mx, s_tab);
+    if (e1 < experts) s.p[e1] = expf_or(l1 - mx, s_tab);
+    __syncthreads();
+    if (wave != 0) return;
+    float p[8];
+    float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int e = lane + 64 * j;
-            if (e < experts && (p[j] > best || (p[j] == best && e < id))) {
-                best = p[j];
-                id = e;
-            }
+    for (int j = 0; j < 8; j++) {
+        const int e = lane + 64 * j;
+        p[j] = 0.0f;
+        if (e < experts) {
+            p[j] = s.p[e];
+            sum = sum + p[j];
         }
-#pragma unroll
-        for (int s = 32; s > 0; s >>= 1) {
-            float v = __shfl_down(best, s, 64);
-            int w = __shfl_down(id, s, 64);
-            if (v > best || (v == best && w < id)) {
-                best = v;
-                id = w;
-            }
-        }
-        best = __shfl(best, 0, 64);
-        id = __shfl(id, 0, 64);
-        if (lane == 0) Ids[k] = id;
-        if (lane == k) mine = best;
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (id == lane + 64 * j) p[j] = -1.0f;
     }
-    float denom = 0.0f;
-    for (int k = 0; k < topK; ++k) denom = denom + __shfl(mine, k, 64);
-    denom = fmaxf(denom, 0.00006103515625f);
-    if (lane < topK) Weights[lane] = mine / denom;
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tree_sum64(sum))));
+    const float inv = 1.0f / sum;
+    int key[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) key[j] = select_key(p[j] * inv, lane + 64 * j < experts);
+    float mine;
+    select_rounds(key, experts, topK, s_ids, mine);
+    router_weights(mine, topK, s_w);
 }
 
 }  // namespace sm

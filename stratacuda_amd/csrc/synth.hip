@@ -40,7 +40,22 @@ __global__ void k_synth_blobs(uint8_t *dst, uint64_t stride, uint64_t code_words
     }
 }
 
+__global__ void k_zero_words(uint32_t *dst, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = 0u;
+}
+
 }  // namespace
+
+namespace smi {
+
+int zero_words(sm_ctx *ctx, void *dst, uint64_t n) {
+    if (!n) return SM_OK;
+    k_zero_words<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>((uint32_t *)dst, n);
+    return launched(ctx);
+}
+
+}  // namespace smi
 
 extern "C" {
 
