@@ -44,10 +44,11 @@ def decode_kernel_bytes(W, F, E, K):
     inputs read + outputs written; logits/hidden intermediates excluded)."""
     gu_blob = 2 * F * W // 4 + 2 * F * (W // 64) * 2
     dn_blob = W * F // 4 + W * (F // 64) * 2
+    xq = (W // 64) * 256                                            # fixed-point activations
     return {
-        "decode_route": E * W * 4 + W * 4 + W * 4 + gu_blob + 4,   # W_r, w_sg, x, shared gate/up plane; gate
-        "decode_gate_up": K * gu_blob + W * 4 + K * 8,             # 10 routed gate/up planes, x; ids, weights
-        "decode_down_combine": (K + 1) * dn_blob + W * 4 + K * 8,  # 11 down planes; y; ids, weights
+        "decode_route": E * W * 4 + W * 4 + W * 4 + xq + 4,              # W_r, w_sg, x; x records, gate
+        "decode_gate_up": (K + 1) * gu_blob + xq + K * 8,                # 10 routed + shared gate/up planes
+        "decode_down_combine": (K + 1) * dn_blob + W * 4 + K * 8,        # 11 down planes; y; ids, weights
     }
 
 

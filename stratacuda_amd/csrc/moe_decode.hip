@@ -2,12 +2,13 @@
 //
 //   K1 k_decode_route   router logits and the shared-expert gate logit in the
 //                       reference's exact f32 order (one wave per row), and, in
-//                       extra blocks of the same grid, the shared expert's
-//                       gate/up rows (they do not depend on the routing).
-//   K2 k_decode_gate_up every block first runs the top-k over the 512 logits
-//                       (router_wave, identical in every block; block 0 also
-//                       publishes ids / weights), then computes hidden rows
-//                       SiLU(g_j . x) * (u_j . x) of one routed expert.
+//                       extra blocks of the same grid, the token's activations
+//                       as per-group fixed point for the integer gate/up dots.
+//   K2 k_decode_gate_up hidden rows SiLU(g_j . x) * (u_j . x) of the topk
+//                       routed experts and the shared one (grid.y = slot).
+//                       Routed blocks first run the top-k over the logits
+//                       (router_block, identical in every block; block (0,0)
+//                       publishes ids / weights); shared blocks start at once.
 //   K3 k_decode_down    each block owns 8 output rows for all topk+1 experts,
 //                       then combines them in the reference order
 //                       (kernels/strata.cu:360-365):
@@ -24,7 +25,8 @@
 // 0-31, the adjacent up row in lanes 32-63: 1 KiB contiguous per wave); in
 // down 8 lanes cover the 8 groups of a 512-wide row and a wave covers 8 rows.
 // Per group the lane accumulates sum(c_i * x_i) over the raw codes c in {0..3}
-// and applies scale * (sum - sum(x_i)) = sum((c_i - 1) * scale * x_i). Every
+// and applies scale * (sum - sum(x_i)) = sum((c_i - 1) * scale * x_i): with
+// int8 dot products against fixed-point x in gate/up, in f32 in down. Every
 // load of a wave is issued before its arithmetic; reductions use DPP.
 #include <hip/hip_runtime.h>
 
@@ -36,9 +38,19 @@ using namespace smi;
 namespace {
 
 // acc += sum over the 16 codes of word w of code * x[i] (code i at bits 2i).
+// (w >> 2k) & 0x03030303 holds codes k, 4+k, 8+k, 12+k in its four bytes,
+// which v_cvt_f32_ubyte0..3 convert directly; the empty asm keeps the
+// compiler from folding the mask back into one bit-field extract per code.
 __device__ __forceinline__ float dot16(uint32_t w, const float *x, float acc) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc = fmaf((float)((w >> (2 * i)) & 3u), x[i], acc);
+    for (int k = 0; k < 4; k++) {
+        uint32_t m = (w >> (2 * k)) & 0x03030303u;
+        asm("" : "+v"(m));
+        acc = fmaf((float)(m & 255u), x[k], acc);
+        acc = fmaf((float)((m >> 8) & 255u), x[4 + k], acc);
+        acc = fmaf((float)((m >> 16) & 255u), x[8 + k], acc);
+        acc = fmaf((float)(m >> 24), x[12 + k], acc);
+    }
     return acc;
 }
 // sum_{i<64} code_i * x_i for one 16-byte code group (two chains for ILP).
@@ -84,27 +96,95 @@ __device__ __forceinline__ const uint8_t *slot_blob(const uint8_t *arena, uint64
     return id >= 0 && id < experts ? arena + (uint64_t)id * stride : nullptr;
 }
 
+// ---------------------------------------------------------------- gate/up
+// The gate/up products run on integer dot products. Each 64-value group g of
+// the token's activations is stored once per step as fixed point:
+//   X_i = rint(x_i * 2^(21 - E_g)),  2^E_g <= max_i |x_i| < 2^(E_g + 1),
+// so |X_i| <= 2^22, split into three balanced base-256 limbs
+// X_i = x0_i + 256 x1_i + 65536 x2_i (each an int8). A 16-code word w of a
+// row holds code 4b + k in byte b of (w >> 2k) & 0x03030303, so one
+// v_dot4_i32_i8 of that mask with the limb bytes of x positions
+// {k, 4 + k, 8 + k, 12 + k} adds four code * limb products. Per group:
+//   sum_i (c_i - 1) X_i = sum_l 256^l sum_i c_i xl_i - sum_i X_i
+// exactly (modulo 2^32 arithmetic; the true value is below 2^30), and the
+// group's contribution is scale_g * (that integer) * 2^(E_g - 21). The only
+// rounding beyond f32 arithmetic is X_i itself (relative 2^-22 of the
+// group's largest value).
+constexpr int XQ_WORDS = 64;  // per group: 48 limb words, scale, sum, padding
+struct XQ {
+    uint32_t limb[48];  // limb[16 l + 4 q + k] byte b: limb l of x[16 q + 4 b + k]
+    float unit;         // 2^(E_g - 21) (0 for an all-zero group, NaN if non-finite)
+    int sum;            // sum_i X_i
+};
+__device__ __forceinline__ void load_xq(const uint32_t *__restrict__ xq, int g, XQ &q) {
+    const uint4 *p = (const uint4 *)(xq + (uint64_t)g * XQ_WORDS);
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+        const uint4 v = p[i];
+        q.limb[4 * i] = v.x;
+        q.limb[4 * i + 1] = v.y;
+        q.limb[4 * i + 2] = v.z;
+        q.limb[4 * i + 3] = v.w;
+    }
+    const uint2 t = *(const uint2 *)(xq + (uint64_t)g * XQ_WORDS + 48);
+    q.unit = __builtin_bit_cast(float, t.x);
+    q.sum = (int)t.y;
+}
+// sum_i (c_i - 1) x_i of one 16-byte code group against quantized x.
+__device__ __forceinline__ float dot64_q(uint4 c, const XQ &q) {
+    int a0 = 0, a1 = 0, a2 = 0;
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int m = (int)((w[qq] >> (2 * k)) & 0x03030303u);
+            a0 = __builtin_amdgcn_sdot4(m, (int)q.limb[4 * qq + k], a0, false);
+            a1 = __builtin_amdgcn_sdot4(m, (int)q.limb[16 + 4 * qq + k], a1, false);
+            a2 = __builtin_amdgcn_sdot4(m, (int)q.limb[32 + 4 * qq + k], a2, false);
+        }
+    }
+    const uint32_t d = (uint32_t)a0 + ((uint32_t)a1 << 8) + ((uint32_t)a2 << 16) - (uint32_t)q.sum;
+    return (float)(int)d * q.unit;
+}
+
+// Quantizes group g of X (one wave, lane i <-> x[64 g + i]) into its record.
+// `bytes` is 192 bytes of this wave's LDS; the caller synchronises the block
+// between the two halves (writes to LDS, then the packed words to memory).
+__device__ __forceinline__ void quantize_group_bytes(const float *__restrict__ X, int g, uint8_t *bytes,
+                                                     float &unit, int &sum) {
+    const int lane = threadIdx.x & 63;
+    const float x = X[g * 64 + lane];
+    const bool bad = __ballot(!(fabsf(x) <= 3.402823466e38f)) != 0;
+    const float m = sm::wave_max(fabsf(x));
+    int X_ = 0;
+    unit = 0.0f;
+    if (bad) {
+        unit = __builtin_nanf("");
+    } else if (m > 0.0f) {
+        const int E = __builtin_amdgcn_frexp_expf(m) - 1;
+        X_ = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(x, 21 - E));
+        unit = __builtin_amdgcn_ldexpf(1.0f, E - 21);
+    }
+    const int l0 = ((X_ + 128) & 255) - 128;
+    const int r1 = (X_ - l0) >> 8;
+    const int l1 = ((r1 + 128) & 255) - 128;
+    const int l2 = (r1 - l1) >> 8;
+    const int q = lane >> 4, b = (lane >> 2) & 3, k = lane & 3;
+    const int at = (4 * q + k) * 4 + b;
+    bytes[at] = (uint8_t)l0;
+    bytes[64 + at] = (uint8_t)l1;
+    bytes[128 + at] = (uint8_t)l2;
+    sum = sm::wave_sum_i32(X_);
+}
+
 constexpr int GU_ROWS = 4;  // hidden rows per wave
 constexpr int GU_WAVES = 4; // waves per block -> 16 hidden rows per block
 
-// The activations of a lane's first group (group lane % 32), loaded before
-// the expert is known so the loads overlap the routing.
-struct XFirst {
-    float x[64];
-    float xs;
-};
-__device__ __forceinline__ void load_x_first(const float *__restrict__ X, int width, XFirst &f) {
-    const int gl = threadIdx.x & 31;
-    f.xs = 0.0f;
-    if (gl < width / 64) {
-        load_group(X + gl * 64, f.x);
-        f.xs = sum64(f.x);
-    }
-}
-
-// Four hidden rows j0..j0+3 of one expert by one wave (width <= 2048 in one
-// pass of the 32 lanes of each half-wave; wider rows loop over groups).
-__device__ __forceinline__ void gate_up_rows(const float *__restrict__ X, const XFirst &xf, const uint8_t *blob,
+// Four hidden rows j0..j0+3 of one expert by one wave. Lane (half = lane/32,
+// gl = lane%32) covers group gl (then gl + 32, ...) of gate row j (half 0)
+// or up row j (half 1); `first` is the lane's first group, loaded early.
+__device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, const XQ &first, const uint8_t *blob,
                                              uint64_t gu_scales, float *__restrict__ hidden_row, int j0, int width,
                                              int ff, const uint64_t *tab) {
     const int lane = threadIdx.x & 63, half = lane >> 5, gl = lane & 31;
@@ -113,7 +193,7 @@ __device__ __forceinline__ void gate_up_rows(const float *__restrict__ X, const 
     float acc[GU_ROWS];
 #pragma unroll
     for (int r = 0; r < GU_ROWS; r++) acc[r] = 0.0f;
-    auto group = [&](int g, const float *x, float xs) {
+    auto group = [&](int g, const XQ &q) {
         uint4 c[GU_ROWS];
         uint32_t sb[GU_ROWS];
 #pragma unroll
@@ -123,14 +203,14 @@ __device__ __forceinline__ void gate_up_rows(const float *__restrict__ X, const 
             sb[r] = *(const uint16_t *)(blob + gu_scales + ((uint64_t)wrow * G + g) * 2);
         }
 #pragma unroll
-        for (int r = 0; r < GU_ROWS; r++) acc[r] = fmaf(sm::half_bits(sb[r]), dot64(c[r], x) - xs, acc[r]);
+        for (int r = 0; r < GU_ROWS; r++) acc[r] = fmaf(sm::half_bits(sb[r]), dot64_q(c[r], q), acc[r]);
     };
     if (blob) {
-        if (gl < G) group(gl, xf.x, xf.xs);
+        if (gl < G) group(gl, first);
         for (int g = gl + 32; g < G; g += 32) {
-            float x[64];
-            load_group(X + g * 64, x);
-            group(g, x, sum64(x));
+            XQ q;
+            load_xq(xq, g, q);
+            group(g, q);
         }
     }
 #pragma unroll
@@ -144,24 +224,29 @@ __device__ __forceinline__ void gate_up_rows(const float *__restrict__ X, const 
 }
 
 // K1. Blocks [0, route_blocks): 4 router rows each (row `experts` = shared
-// gate, exact reference order). Blocks after that: shared-expert gate/up,
-// 16 hidden rows per block.
+// gate), one wave per row in the reference's exact f32 order. Blocks after
+// that: one wave per 64-value group of X writes the group's fixed-point record.
 template <int NJ>
 __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ X, const float *__restrict__ Wr,
                                                       const float *__restrict__ bias, const float *__restrict__ Wsg,
-                                                      const uint8_t *__restrict__ shared_blob,
                                                       float *__restrict__ logits, float *__restrict__ gate_out,
-                                                      float *__restrict__ hidden_shared, int width, int ff,
-                                                      int experts, int route_blocks, uint64_t gu_scales) {
+                                                      uint32_t *__restrict__ xq, int width, int experts,
+                                                      int route_blocks) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if ((int)blockIdx.x >= route_blocks) {
-        __shared__ uint64_t s_tab[32];
-        XFirst xf;
-        load_x_first(X, width, xf);
-        if (threadIdx.x < 32) s_tab[threadIdx.x] = sm::kExp2Tab[threadIdx.x];
+        __shared__ uint8_t s_bytes[4][192];
+        const int g = ((int)blockIdx.x - route_blocks) * 4 + wave;
+        const bool live = g < width / 64;
+        float unit = 0.0f;
+        int sum = 0;
+        if (live) quantize_group_bytes(X, g, s_bytes[wave], unit, sum);
         __syncthreads();
-        const int j0 = ((blockIdx.x - route_blocks) * GU_WAVES + wave) * GU_ROWS;
-        if (j0 < ff) gate_up_rows(X, xf, shared_blob, gu_scales, hidden_shared, j0, width, ff, s_tab);
+        if (live) {
+            uint32_t *rec = xq + (uint64_t)g * XQ_WORDS;
+            if (lane < 48) rec[lane] = ((const uint32_t *)s_bytes[wave])[lane];
+            else if (lane == 48) rec[48] = __builtin_bit_cast(uint32_t, unit);
+            else if (lane == 49) rec[49] = (uint32_t)sum;
+        }
         return;
     }
     const int row = blockIdx.x * 4 + wave;
@@ -186,103 +271,49 @@ __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ 
     }
 }
 
-// K2. Grid (ceil(ff / 16), topk). Wave 0 runs the top-k into LDS (block (0,0)
-// also writes ids / weights to memory); then every wave computes 4 hidden
-// rows of routed expert blockIdx.y.
-__global__ void __launch_bounds__(256) k_decode_gate_up(const float *__restrict__ X, const uint8_t *__restrict__ arena,
-                                                        uint64_t stride, const float *__restrict__ logits,
-                                                        int *__restrict__ ids, float *__restrict__ weights,
-                                                        float *__restrict__ hidden, int width, int ff, int topk,
-                                                        int experts, uint64_t gu_scales) {
+// K2. Grid (ceil(ff / 16), topk + 1). Slot blockIdx.y < topk: wave 0 runs the
+// top-k into LDS (block (0,0) also writes ids / weights to memory), then every
+// wave computes 4 hidden rows of that routed expert. Slot topk is the shared
+// expert and needs no routing.
+__global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restrict__ xq,
+                                                        const uint8_t *__restrict__ arena, uint64_t stride,
+                                                        const uint8_t *__restrict__ shared_blob,
+                                                        const float *__restrict__ logits, int *__restrict__ ids,
+                                                        float *__restrict__ weights, float *__restrict__ hidden,
+                                                        int width, int ff, int topk, int experts, uint64_t gu_scales) {
     __shared__ int s_ids[32];
     __shared__ float s_w[32];
     __shared__ uint64_t s_tab[32];
     __shared__ sm::RouterScratch s_router;
-    const int wave = threadIdx.x >> 6;
-    const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
-    XFirst xf;
-    load_x_first(X, width, xf);
-    if (threadIdx.x < 32) s_tab[threadIdx.x] = sm::kExp2Tab[threadIdx.x];
-    sm::router_block(logits, experts, topk, s_tab, s_router, s_ids, s_w);
-    __syncthreads();
-    if (publish && (int)threadIdx.x < topk) {
-        ids[threadIdx.x] = s_ids[threadIdx.x];
-        weights[threadIdx.x] = s_w[threadIdx.x];
-    }
+    const int wave = threadIdx.x >> 6, gl = threadIdx.x & 31;
     const int k = blockIdx.y;
-    const uint8_t *blob = slot_blob(arena, stride, nullptr, s_ids[k], k, topk, experts);
-    const int j0 = (blockIdx.x * GU_WAVES + wave) * GU_ROWS;
-    if (j0 < ff) gate_up_rows(X, xf, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
-}
-
-// K3. Grid ceil(width / 8), 256 threads: wave w handles experts w, w+4, ...
-// Lane (r = lane / 8, gl = lane % 8) covers groups gl, gl+8, ... of down row
-// r. All code loads of a wave are issued first; partial rows go to LDS and are
-// combined in the reference order.
-constexpr int DN_MAX_SLOTS = 9;  // experts per wave with up-front loads (33 slots / 4 waves)
-__global__ void __launch_bounds__(256) k_decode_down(const float *__restrict__ hidden, const uint8_t *__restrict__ arena,
-                                                     uint64_t stride, const uint8_t *__restrict__ shared_blob,
-                                                     const int *__restrict__ ids, const float *__restrict__ weights,
-                                                     const float *__restrict__ gate, float *__restrict__ Y, int width,
-                                                     int ff, int topk, int experts, uint64_t down_codes,
-                                                     uint64_t down_scales) {
-    __shared__ float parts[33 * 8];
-    __shared__ uint64_t s_tab[32];
-    const int nexp = topk + 1, GF = ff / 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < 32) s_tab[tid] = sm::kExp2Tab[tid];
-    const int r = min((int)blockIdx.x * 8 + (lane >> 3), width - 1), gl = lane & 7;
-    const uint64_t row_bytes = (uint64_t)ff / 4;
-    if (GF <= 8) {
-        // One group per lane: issue every code load of this wave first.
-        uint4 c[DN_MAX_SLOTS];
-        uint32_t sb[DN_MAX_SLOTS];
-        const uint8_t *blobs[DN_MAX_SLOTS];
-#pragma unroll
-        for (int q = 0; q < DN_MAX_SLOTS; q++) {
-            const int k = wave + 4 * q;
-            blobs[q] = nullptr;
-            c[q] = make_uint4(0, 0, 0, 0);
-            sb[q] = 0;
-            if (k < nexp) {
-                blobs[q] = slot_blob(arena, stride, shared_blob, k < topk ? ids[k] : 0, k, topk, experts);
-                if (blobs[q] && gl < GF) {
-                    c[q] = load_codes(blobs[q] + down_codes + (uint64_t)r * row_bytes + (uint64_t)gl * 16);
-                    sb[q] = *(const uint16_t *)(blobs[q] + down_scales + ((uint64_t)r * GF + gl) * 2);
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < DN_MAX_SLOTS; q++) {
-            const int k = wave + 4 * q;
-            if (k >= nexp) break;
-            float v = blobs[q] ? 0.0f : __builtin_nanf("");
-            if (blobs[q] && gl < GF) {
-                float h[64];
-                load_group(hidden + (uint64_t)k * ff + gl * 64, h);
-                v = sm::half_bits(sb[q]) * (dot64(c[q], h) - sum64(h));
-            }
-            v = sm::group8_sum(v);
-            if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
+    float l0 = 0.0f, l1 = 0.0f;
+    if (k < topk) sm::router_load(logits, experts, l0, l1);
+    XQ first;
+    if (gl < width / 64) load_xq(xq, gl, first);
+    sm::fill_exp_table(s_tab);
+    if (k < topk) {
+        sm::router_block(l0, l1, experts, topk, s_tab, s_router, s_ids, s_w);
+        __syncthreads();
+        if (blockIdx.x == 0 && k == 0 && (int)threadIdx.x < topk) {
+            ids[threadIdx.x] = s_ids[threadIdx.x];
+            weights[threadIdx.x] = s_w[threadIdx.x];
         }
     } else {
-        for (int k = wave; k < nexp; k += 4) {
-            const uint8_t *blob = slot_blob(arena, stride, shared_blob, k < topk ? ids[k] : 0, k, topk, experts);
-            float v = blob ? 0.0f : __builtin_nanf("");
-            if (blob) {
-                for (int g = gl; g < GF; g += 8) {
-                    const uint4 c = load_codes(blob + down_codes + (uint64_t)r * row_bytes + (uint64_t)g * 16);
-                    const uint32_t sb = *(const uint16_t *)(blob + down_scales + ((uint64_t)r * GF + g) * 2);
-                    float h[64];
-                    load_group(hidden + (uint64_t)k * ff + g * 64, h);
-                    v = fmaf(sm::half_bits(sb), dot64(c, h) - sum64(h), v);
-                }
-            }
-            v = sm::group8_sum(v);
-            if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
-        }
+        __syncthreads();
     }
-    __syncthreads();
+    const uint8_t *blob = slot_blob(arena, stride, shared_blob, k < topk ? s_ids[k] : 0, k, topk, experts);
+    const int j0 = (blockIdx.x * GU_WAVES + wave) * GU_ROWS;
+    if (j0 < ff)
+        gate_up_rows(xq, first, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
+}
+
+// K3, the combine at its end shared by both variants (kernels/strata.cu:360-365):
+// y = shared * sigmoid(gate) + sum_k part_k * w_k, in that order.
+__device__ __forceinline__ void down_combine(const float *parts, const float *__restrict__ weights,
+                                             const float *__restrict__ gate, float *__restrict__ Y, int width,
+                                             int topk, const uint64_t *s_tab) {
+    const int tid = threadIdx.x;
     if (tid < 8) {
         const int row = blockIdx.x * 8 + tid;
         if (row < width) {
@@ -293,18 +324,109 @@ __global__ void __launch_bounds__(256) k_decode_down(const float *__restrict__ h
     }
 }
 
+// K3 for ff <= 512 (one 64-value group per lane). Grid ceil(width / 8),
+// 256 threads, 8 output rows per block. Wave w handles slots w, w+4, ...;
+// lane (r = lane / 8, gl = lane % 8) dots group gl of down row r with group gl
+// of the slot's hidden vector. The slot IDs are wave-uniform scalar loads;
+// every code group of the wave is requested before any arithmetic, and each
+// slot's hidden group is loaded as its turn comes. Partial rows meet in LDS
+// for the combine.
+constexpr int DN_MAX_SLOTS = 9;  // slots per wave (33 slots / 4 waves)
+__global__ void __launch_bounds__(256) k_decode_down(const float *__restrict__ hidden, const uint8_t *__restrict__ arena,
+                                                     uint64_t stride, const uint8_t *__restrict__ shared_blob,
+                                                     const int *__restrict__ ids, const float *__restrict__ weights,
+                                                     const float *__restrict__ gate, float *__restrict__ Y, int width,
+                                                     int ff, int topk, int experts, uint64_t down_codes,
+                                                     uint64_t down_scales) {
+    __shared__ float parts[33 * 8];
+    __shared__ uint64_t s_tab[32];
+    const int nexp = topk + 1, GF = ff / 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = min((int)blockIdx.x * 8 + (lane >> 3), width - 1), gl = lane & 7;
+    const uint64_t row_bytes = (uint64_t)ff / 4;
+    uint4 c[DN_MAX_SLOTS];
+    uint32_t sb[DN_MAX_SLOTS];
+    const uint8_t *blobs[DN_MAX_SLOTS];
+#pragma unroll
+    for (int q = 0; q < DN_MAX_SLOTS; q++) {
+        const int k = wave + 4 * q;
+        blobs[q] = nullptr;
+        c[q] = make_uint4(0, 0, 0, 0);
+        sb[q] = 0;
+        if (k < nexp) {
+            blobs[q] = slot_blob(arena, stride, shared_blob, k < topk ? ids[k] : 0, k, topk, experts);
+            if (blobs[q] && gl < GF) {
+                c[q] = load_codes(blobs[q] + down_codes + (uint64_t)r * row_bytes + (uint64_t)gl * 16);
+                sb[q] = *(const uint16_t *)(blobs[q] + down_scales + ((uint64_t)r * GF + gl) * 2);
+            }
+        }
+    }
+    sm::fill_exp_table(s_tab);
+#pragma unroll
+    for (int q = 0; q < DN_MAX_SLOTS; q++) {
+        const int k = wave + 4 * q;
+        if (k >= nexp) break;
+        float v = blobs[q] ? 0.0f : __builtin_nanf("");
+        if (blobs[q] && gl < GF) {
+            float h[64];
+            load_group(hidden + (uint64_t)k * ff + gl * 64, h);
+            v = sm::half_bits(sb[q]) * (dot64(c[q], h) - sum64(h));
+        }
+        v = sm::group8_sum(v);
+        if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
+    }
+    __syncthreads();
+    down_combine(parts, weights, gate, Y, width, topk, s_tab);
+}
+
+// K3 for any other shape: hidden groups read from memory, lanes loop over
+// groups gl, gl+8, ... of row r.
+__global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restrict__ hidden,
+                                                          const uint8_t *__restrict__ arena, uint64_t stride,
+                                                          const uint8_t *__restrict__ shared_blob,
+                                                          const int *__restrict__ ids, const float *__restrict__ weights,
+                                                          const float *__restrict__ gate, float *__restrict__ Y,
+                                                          int width, int ff, int topk, int experts, uint64_t down_codes,
+                                                          uint64_t down_scales) {
+    __shared__ float parts[33 * 8];
+    __shared__ uint64_t s_tab[32];
+    const int nexp = topk + 1, GF = ff / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    sm::fill_exp_table(s_tab);
+    const int r = min((int)blockIdx.x * 8 + (lane >> 3), width - 1), gl = lane & 7;
+    const uint64_t row_bytes = (uint64_t)ff / 4;
+    for (int k = wave; k < nexp; k += 4) {
+        const uint8_t *blob = slot_blob(arena, stride, shared_blob, k < topk ? ids[k] : 0, k, topk, experts);
+        float v = blob ? 0.0f : __builtin_nanf("");
+        if (blob) {
+            for (int g = gl; g < GF; g += 8) {
+                const uint4 c = load_codes(blob + down_codes + (uint64_t)r * row_bytes + (uint64_t)g * 16);
+                const uint32_t sb = *(const uint16_t *)(blob + down_scales + ((uint64_t)r * GF + g) * 2);
+                float h[64];
+                load_group(hidden + (uint64_t)k * ff + g * 64, h);
+                v = fmaf(sm::half_bits(sb), dot64(c, h) - sum64(h), v);
+            }
+        }
+        v = sm::group8_sum(v);
+        if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
+    }
+    __syncthreads();
+    down_combine(parts, weights, gate, Y, width, topk, s_tab);
+}
+
 constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct DecodeWs {
-    uint64_t logits, gate, hidden, end;
+    uint64_t logits, gate, xq, hidden, end;
 };
 DecodeWs decode_ws(int width, int ff, int experts, int topk) {
-    (void)width;
     DecodeWs w;
     w.logits = 0;
     w.gate = up(w.logits + (uint64_t)experts * 4);
-    w.hidden = up(w.gate + 4);
+    w.xq = up(w.gate + 4);
+    w.hidden = up(w.xq + (uint64_t)(width / 64) * XQ_WORDS * 4);
     w.end = up(w.hidden + (uint64_t)(topk + 1) * ff * 4);
     return w;
 }
@@ -324,37 +446,36 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
     BlobLayout L = blob_layout(width, ff);
     float *hidden = (float *)(ws + w.hidden);
     const int blocks_per_expert = ceil_div(ff, GU_ROWS * GU_WAVES);
-    // 1. router logits + shared gate logit + shared-expert gate/up
+    uint32_t *xq = (uint32_t *)(ws + w.xq);
+    // 1. router logits + shared gate logit + fixed-point activations
     if (stage_on(ctx, kStageDecodeRoute)) {
         if (int rc = stage_mark(ctx, kStageDecodeRoute)) return rc;
         const int route_blocks = ceil_div(experts + 1, 4);
-        const unsigned grid = (unsigned)(route_blocks + blocks_per_expert);
+        const unsigned grid = (unsigned)(route_blocks + ceil_div(width / 64, 4));
         if (width == 2048)
             k_decode_route<32><<<grid, 256, 0, ctx->stream>>>(
-                (const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg,
-                (const uint8_t *)shared_blob, (float *)(ws + w.logits), (float *)(ws + w.gate),
-                hidden + (uint64_t)topk * ff, width, ff, experts, route_blocks, L.gate_up_scales);
+                (const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg, (float *)(ws + w.logits),
+                (float *)(ws + w.gate), xq, width, experts, route_blocks);
         else
             k_decode_route<0><<<grid, 256, 0, ctx->stream>>>(
-                (const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg,
-                (const uint8_t *)shared_blob, (float *)(ws + w.logits), (float *)(ws + w.gate),
-                hidden + (uint64_t)topk * ff, width, ff, experts, route_blocks, L.gate_up_scales);
+                (const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg, (float *)(ws + w.logits),
+                (float *)(ws + w.gate), xq, width, experts, route_blocks);
         if (int rc = launched(ctx)) return rc;
     }
-    // 2. top-k (per block) + gate/up of the routed experts
+    // 2. top-k (per routed block) + gate/up of the routed and shared experts
     if (stage_on(ctx, kStageDecodeGateUp)) {
         if (int rc = stage_mark(ctx, kStageDecodeGateUp)) return rc;
-        dim3 g1((unsigned)blocks_per_expert, (unsigned)topk);
-        k_decode_gate_up<<<g1, 64 * GU_WAVES, 0, ctx->stream>>>((const float *)X, (const uint8_t *)arena, blob_stride,
-                                                                (const float *)(ws + w.logits), (int *)ids,
-                                                                (float *)weights, hidden, width, ff, topk, experts,
-                                                                L.gate_up_scales);
+        dim3 g1((unsigned)blocks_per_expert, (unsigned)(topk + 1));
+        k_decode_gate_up<<<g1, 64 * GU_WAVES, 0, ctx->stream>>>(
+            xq, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const float *)(ws + w.logits),
+            (int *)ids, (float *)weights, hidden, width, ff, topk, experts, L.gate_up_scales);
         if (int rc = launched(ctx)) return rc;
     }
     // 3. down for all experts + combine
     if (stage_on(ctx, kStageDecodeDown)) {
         if (int rc = stage_mark(ctx, kStageDecodeDown)) return rc;
-        k_decode_down<<<(unsigned)ceil_div(width, 8), 256, 0, ctx->stream>>>(
+        auto kernel = ff <= 512 ? k_decode_down : k_decode_down_wide;
+        kernel<<<(unsigned)ceil_div(width, 8), 256, 0, ctx->stream>>>(
             hidden, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const int *)ids,
             (const float *)weights, (const float *)(ws + w.gate), (float *)Y, width, ff, topk, experts, L.down_codes,
             L.down_scales);

@@ -131,7 +131,7 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
 __global__ void __launch_bounds__(256) k_topk(const float *__restrict__ logits, int *__restrict__ ids,
                                               float *__restrict__ weights, int tokens, int experts, int topk) {
     __shared__ uint64_t s_tab[32];
-    if (threadIdx.x < 32) s_tab[threadIdx.x] = sm::kExp2Tab[threadIdx.x];
+    sm::fill_exp_table(s_tab);
     __syncthreads();
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;

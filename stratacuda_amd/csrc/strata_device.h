@@ -75,6 +75,18 @@ __device__ __forceinline__ float expf_or(float x, const uint64_t *tab = kExp2Tab
     y = y * s;
     return (float)y;
 }
+// Fills an LDS copy of kExp2Tab (threads 0-31, one entry each) from values
+// known at compile time: no vector-memory load, so nothing delays the
+// kernel's first loads.
+__device__ __forceinline__ void fill_exp_table(uint64_t *s_tab) {
+    const int t = threadIdx.x;
+    if (t < 32) {
+        uint64_t v = kExp2Tab[0];
+#pragma unroll
+        for (int i = 1; i < 32; i++) v = t == i ? kExp2Tab[i] : v;
+        s_tab[t] = v;
+    }
+}
 // kernels/strata.cu:7-8
 __device__ __forceinline__ float sigmoid(float x, const uint64_t *tab = kExp2Tab) {
     return 1.0f / (1.0f + expf_or(-x, tab));
@@ -106,10 +118,15 @@ __device__ __forceinline__ int dpp_i32(int old, int v) {
 // Tree sum over the 64 lanes in the reference order (s = 32, 16, ..., 1: lane
 // l adds lane l+s), so the result is bit-identical to the reference's
 // shared-memory tree. Valid in lane 0. Levels 8..1 stay inside a 16-lane row
-// (DPP row_shl: lane i receives lane i+s); levels 32 and 16 cross rows.
+// (DPP row_shl: lane i receives lane i+s); levels 32 and 16 cross rows
+// through the gfx950 lane-swap instructions.
 __device__ __forceinline__ float tree_sum64(float v) {
-    v = v + __shfl_down(v, 32, 64);
-    v = v + __shfl_down(v, 16, 64);
+    // v_permlane32_swap(v, v).second holds lane l+32 in lanes 0-31;
+    // v_permlane16_swap(v, v).second holds lane l+16 in rows 0 and 2.
+    v = v + __builtin_bit_cast(float, (int)__builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v),
+                                                                          __builtin_bit_cast(int, v), false, false)[1]);
+    v = v + __builtin_bit_cast(float, (int)__builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v),
+                                                                          __builtin_bit_cast(int, v), false, false)[1]);
     v = v + dpp_f32<0x108>(0.0f, v);
     v = v + dpp_f32<0x104>(0.0f, v);
     v = v + dpp_f32<0x102>(0.0f, v);
@@ -134,6 +151,26 @@ __device__ __forceinline__ int wave_min_i32(int v) {
     v = min(v, dpp_i32<kDppRowBcast15, 0xa>(v, v));
     v = min(v, dpp_i32<kDppRowBcast31, 0xc>(v, v));
     return __builtin_amdgcn_readlane(v, 63);
+}
+// Exact integer sum over the wave, in every lane.
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    v = v + dpp_i32<kDppQuadXor1>(0, v);
+    v = v + dpp_i32<kDppQuadXor2>(0, v);
+    v = v + dpp_i32<kDppRowHalfMirror>(0, v);
+    v = v + dpp_i32<kDppRowMirror>(0, v);
+    v = v + dpp_i32<kDppRowBcast15, 0xa>(0, v);
+    v = v + dpp_i32<kDppRowBcast31, 0xc>(0, v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t u) {
+    int v = (int)u;
+    v = (int)max((uint32_t)v, (uint32_t)dpp_i32<kDppQuadXor1>(v, v));
+    v = (int)max((uint32_t)v, (uint32_t)dpp_i32<kDppQuadXor2>(v, v));
+    v = (int)max((uint32_t)v, (uint32_t)dpp_i32<kDppRowHalfMirror>(v, v));
+    v = (int)max((uint32_t)v, (uint32_t)dpp_i32<kDppRowMirror>(v, v));
+    v = (int)max((uint32_t)v, (uint32_t)dpp_i32<kDppRowBcast15, 0xa>(v, v));
+    v = (int)max((uint32_t)v, (uint32_t)dpp_i32<kDppRowBcast31, 0xc>(v, v));
+    return (uint32_t)__builtin_amdgcn_readlane(v, 63);
 }
 __device__ __forceinline__ int wave_max_i32(int v) {
     v = max(v, dpp_i32<kDppQuadXor1>(v, v));
@@ -206,46 +243,63 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 
 // Selection keys for the reference's top-k rounds (kernels/strata.cu:252-265).
 // A probability p >= +0 is keyed by its bit pattern read as int, which orders
-// exactly like the value; a selected expert holds -1.0f (kPickedKey, negative
-// as int, still above every key below); an expert past `experts` or with a NaN
-// probability gets INT_MIN, which the reference's `>` / `==` tests never pick.
-// kNoKey sits between the two: it is a lane's starting best, so a lane picks
-// the first selected (-1.0f) entry when nothing larger is left, as the
-// reference does, and keeps kNoKey (ID = experts) when it has no entry at all.
-constexpr int kPickedKey = (int)0xBF800000u;
-constexpr int kNoKey = kPickedKey - 1;
+// exactly like the value; an expert past `experts` or with a NaN probability
+// gets kNoneKey (INT_MIN), which the reference's `>` / `==` tests never pick.
+constexpr int kNoneKey = (int)0x80000000u;
 __device__ __forceinline__ int select_key(float p, bool valid) {
-    return valid && p == p ? __builtin_bit_cast(int, p) : (int)0x80000000u;
+    return valid && p == p ? __builtin_bit_cast(int, p) : kNoneKey;
 }
-// topK selection rounds over one wave; lane l holds the keys of experts
-// l + 64 j. Each round: every lane's best (first j among equal keys, i.e.
-// the lower ID), the wave maximum, and among lanes tied at the maximum the
-// lowest ID; that expert's key becomes kPickedKey. Lane 0 writes Ids[k];
-// lane k returns the selected probability of round k in `mine`.
-__device__ __forceinline__ void select_rounds(int (&key)[8], int experts, int topK, int *Ids, float &mine) {
+// Sorts eight packed entries in descending order (Batcher's odd-even merge
+// network, 19 compare-exchanges; all registers, no branches).
+__device__ __forceinline__ void sort8_desc(uint64_t (&P)[8]) {
+    constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                                 {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+    for (int c = 0; c < 19; c++) {
+        const uint64_t a = P[kNet[c][0]], b = P[kNet[c][1]];
+        const bool swap = b > a;
+        P[kNet[c][0]] = swap ? b : a;
+        P[kNet[c][1]] = swap ? a : b;
+    }
+}
+// topK selection rounds over one wave, with the reference's results; lane l
+// holds the keys of experts l + 64 j (j < 8). The reference takes, each
+// round, the largest probability (lower ID on ties) and sets it to -1.0f.
+// Here every lane first sorts its eight entries, packed as
+// (key ^ 2^31) << 3 | (7 - j), so its head is its best entry (the lower j,
+// hence the lower ID, on equal keys). A round is then one wave maximum over
+// the heads, a ballot for ties between lanes (the lowest ID among tied heads
+// wins) and a shift of the winning lane's list. Once no entry with p >= 0 is
+// left, the reference's rounds pick the lowest-ID expert already set to -1.0f
+// (or ID `experts` when there is none), which `lowest_picked` tracks.
+// Lane 0 writes Ids[k]; lane k returns the selected probability of round k.
+__device__ __forceinline__ void select_rounds(const int (&key)[8], int experts, int topK, int *Ids, float &mine) {
     const int lane = threadIdx.x & 63;
+    uint64_t P[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) P[j] = ((uint64_t)((uint32_t)key[j] ^ 0x80000000u) << 3) | (uint64_t)(7 - j);
+    sort8_desc(P);
+    int lowest_picked = experts;
     mine = 0.0f;
     for (int k = 0; k < topK; ++k) {
-        int best = kNoKey, bj = 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const bool gt = key[j] > best;
-            best = gt ? key[j] : best;
-            bj = gt ? j : bj;
-        }
-        const int top = wave_max_i32(best);
-        int winner = experts;
-        if (top != kNoKey) {
-            const unsigned long long tied = __ballot(best == top);
-            const int id = lane + 64 * bj;
+        const uint32_t head = (uint32_t)(P[0] >> 3);
+        const uint32_t top = wave_max_u32(head);
+        int winner = lowest_picked;
+        float value = -1.0f;
+        if (top != 0u) {
+            const unsigned long long tied = __ballot(head == top);
+            const int id = lane + 64 * (7 - (int)(P[0] & 7u));
             if (__popcll(tied) == 1) winner = __builtin_amdgcn_readlane(id, __ffsll((long long)tied) - 1);
-            else winner = wave_min_i32(best == top ? id : 0x7fffffff);
+            else winner = wave_min_i32(head == top ? id : 0x7fffffff);
+            value = __builtin_bit_cast(float, top ^ 0x80000000u);
+            lowest_picked = min(lowest_picked, winner);
+            const bool pop = lane == (winner & 63);
+#pragma unroll
+            for (int j = 0; j < 7; j++) P[j] = pop ? P[j + 1] : P[j];
+            P[7] = pop ? 0ull : P[7];
         }
         if (lane == 0) Ids[k] = winner;
-        if (lane == k) mine = top == kNoKey ? -1.0f : __builtin_bit_cast(float, top);
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (winner == lane + 64 * j) key[j] = kPickedKey;
+        if (lane == k) mine = value;
     }
 }
 // kernels/strata.cu:266-269: weights = selected / max(sum(selected), 2^-14),
@@ -300,20 +354,102 @@ __device__ __forceinline__ void router_wave(const float *Logits, int *Ids, float
     router_weights(mine, topK, Weights);
 }
 
+// Orders LDS accesses of one wave (no other wave takes part): the fences
+// keep the compiler from moving LDS reads and writes across this point, and
+// a wave's LDS instructions complete in order.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// LDS for router_block: probabilities, the cross-wave max, and the scratch of
+// select_ranked.
+struct RouterScratch {
+    float p[512];
+    float red[4];
+    uint64_t cand[64];
+    int ids[32];
+    float val[32];
+};
+
+// The same selection as select_rounds in one pass. Entry e gets the 41-bit
+// order key Q = (key ^ 2^31) << 9 | (511 - e): Q descending is exactly the
+// order in which the reference's rounds pick experts (larger probability
+// first, lower ID on equal probabilities), so round k picks the entry of
+// rank k. The topK largest entries all have a key >= T, the topK-th largest
+// of the 64 lane maxima (those maxima are topK distinct entries); T comes
+// from a bitwise search with ballots. The entries with key >= T are gathered
+// in LDS (one per lane) and each is ranked against the others. With more
+// than 64 such entries (heavy ties), or when T belongs to an invalid entry
+// (no probability >= 0 among them: NaN routing input), the rounds of
+// select_rounds run instead.
+__device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, int topK, RouterScratch &x,
+                                              int *s_ids, float &mine) {
+    const int lane = threadIdx.x & 63;
+    uint32_t hk = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) hk = max(hk, (uint32_t)key[j] ^ 0x80000000u);
+    uint32_t T = 0;
+#pragma unroll
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t c = T | (1u << b);
+        if (__popcll(__ballot(hk >= c)) >= topK) T = c;
+    }
+    int count = 0;
+    uint64_t Q[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t k = (uint32_t)key[j] ^ 0x80000000u;
+        Q[j] = ((uint64_t)k << 9) | (uint64_t)(511 - (lane + 64 * j));
+        count += __popcll(__ballot(k >= T));
+    }
+    if (T < 0x80000000u || count > 64) {
+        select_rounds(key, experts, topK, s_ids, mine);
+        return;
+    }
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const bool in = (uint32_t)(Q[j] >> 9) >= T;
+        const unsigned long long m = __ballot(in);
+        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+        if (in) x.cand[base + below] = Q[j];
+        base += __popcll(m);
+    }
+    wave_lds_sync();
+    if (lane < count) {
+        const uint64_t q = x.cand[lane];
+        int rank = 0;
+        for (int m = 0; m < count; m++) rank += x.cand[m] > q ? 1 : 0;
+        if (rank < topK) {
+            x.ids[rank] = 511 - (int)(q & 511u);
+            x.val[rank] = __builtin_bit_cast(float, (uint32_t)(q >> 9) ^ 0x80000000u);
+        }
+    }
+    wave_lds_sync();
+    mine = 0.0f;
+    if (lane < topK) {
+        s_ids[lane] = x.ids[lane];
+        mine = x.val[lane];
+    }
+}
+
 // The same routing for one token by a 256-thread block: the 512 exponentials
 // are spread over all threads (table in LDS), wave 0 forms the reference sum
 // and runs the selection rounds. Results land in s_ids / s_w (LDS). Needs
 // blockDim.x == 256 and experts <= 512. s_tab must already hold kExp2Tab.
-struct RouterScratch {
-    float p[512];
-    float red[4];
-};
-__device__ __forceinline__ void router_block(const float *Logits, int experts, int topK, const uint64_t *s_tab,
+// Thread t's logits (experts t and t + 256); issued before a kernel's other
+// loads, as vector loads complete in order.
+__device__ __forceinline__ void router_load(const float *Logits, int experts, float &l0, float &l1) {
+    const int e0 = threadIdx.x, e1 = threadIdx.x + 256;
+    l0 = e0 < experts ? Logits[e0] : -3.402823e38f;
+    l1 = e1 < experts ? Logits[e1] : -3.402823e38f;
+}
+__device__ __forceinline__ void router_block(float l0, float l1, int experts, int topK, const uint64_t *s_tab,
                                              RouterScratch &s, int *s_ids, float *s_w) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int e0 = tid, e1 = tid + 256;
-    const float l0 = e0 < experts ? Logits[e0] : -3.402823e38f;
-    const float l1 = e1 < experts ? Logits[e1] : -3.402823e38f;
     float mx = wave_max(fmaxf(l0, l1));
     if (lane == 0) s.red[wave] = mx;
     __syncthreads();
@@ -339,7 +475,7 @@ __device__ __forceinline__ void router_block(const float *Logits, int experts, i
 #pragma unroll
     for (int j = 0; j < 8; j++) key[j] = select_key(p[j] * inv, lane + 64 * j < experts);
     float mine;
-    select_rounds(key, experts, topK, s_ids, mine);
+    select_ranked(key, experts, topK, s, s_ids, mine);
     router_weights(mine, topK, s_w);
 }
 

@@ -139,7 +139,7 @@ def test_norm_and_elementwise(backend, oracle):
         same(backend.read(Y), oracle.elementwise(A, B, mode, 1.25))
 
 
-@pytest.mark.parametrize("style", ["ties", "spread", "random", "small"])
+@pytest.mark.parametrize("style", ["ties", "spread", "random", "small", "nonfinite"])
 def test_router_and_batch(backend, oracle, style):
     rng = np.random.default_rng(4)
     experts, k, tokens = (6, 2, 5) if style == "small" else (512, 10, 37)
@@ -149,6 +149,18 @@ def test_router_and_batch(backend, oracle, style):
         logits = np.tile((np.sin(np.arange(experts) * 3.1) * 90).astype(np.float32), tokens)
     else:
         logits = rng.normal(0, 1, tokens * experts).astype(np.float32)
+    if style == "nonfinite":
+        # NaN anywhere makes every probability NaN (ID `experts` each round);
+        # -inf logits give probability 0, so the last rounds break ties at 0
+        # by the lower ID; +inf makes the max inf and every probability NaN.
+        t = logits.reshape(tokens, experts)
+        t[0, 3] = np.nan
+        t[1, :] = np.nan
+        t[2, 5:] = -np.inf
+        t[3, 100] = np.inf
+        t[4, ::2] = -np.inf
+        t[5, :] = -np.inf
+        t[5, 7] = 0.0
     L = backend.alloc(logits)
     ids, w = backend.alloc(tokens * k, "i32"), backend.alloc(tokens * k)
     backend.run("strata_router_batch", {"Logits": L, "Ids": ids, "Weights": w, "experts": experts, "topK": k},
