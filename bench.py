@@ -92,6 +92,92 @@ def cpu_baseline(oracle, wl, seconds):
                       "kernels' f32 operation order, OpenMP over workgroups, %.1f s" % (n, el)}
 
 
+PROFILE_CMDS = {
+    "trace": "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/trace -o decode -- "
+             "python3 -u bench.py --no-cpu --steps 960",
+    "fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o decode -- "
+             "python3 -u bench.py --no-cpu --no-prefill --layers 8 --steps 16 --warmup 8",
+    "write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o decode -- "
+             "python3 -u bench.py --no-cpu --no-prefill --layers 8 --steps 16 --warmup 8",
+    "cal_fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_cal_fetch -o cal -- python3 -u bench.py --calibrate",
+    "cal_write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_cal_write -o cal -- python3 -u bench.py --calibrate",
+}
+DECODE_KERNELS = ["k_decode_route", "k_decode_gate_up", "k_decode_down"]
+
+
+def _csv_rows(path):
+    import csv
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def _kernel_key(name):
+    for k in DECODE_KERNELS + ["k_prefill_gate_up", "k_prefill_down", "k_prefill_route", "k_dispatch",
+                               "k_prefill_combine", "k_elementwise", "strata_elementwise"]:
+        if "::" + k + "(" in name or name.startswith(k + "(") or ("::" + k + "<") in name:
+            return k
+    return None
+
+
+def _pmc_mean(path, counter, kernel):
+    vals = [float(r["Counter_Value"]) for r in _csv_rows(path)
+            if r["Counter_Name"] == counter and _kernel_key(r["Kernel_Name"]) == kernel]
+    return sum(vals) / len(vals) if vals else None, len(vals)
+
+
+def summarize(out_dir):
+    """Turns the rocprofv3 CSVs of the profiling commands (PROFILE_CMDS, run
+    with their output under out_dir) into the text summaries under profiles/:
+    kernel durations, and HBM traffic per launch from FETCH_SIZE / WRITE_SIZE
+    (KiB per dispatch) scaled by what the same counters read for the copy
+    kernel of known size."""
+    import glob
+    prof = os.path.join(ROOT, "profiles")
+    os.makedirs(prof, exist_ok=True)
+    stats = glob.glob(os.path.join(out_dir, "trace", "*kernel_stats.csv"))
+    lines = ["# Kernel durations: decode T=1 (48 rotated layers) and prefill T=512 / T=2048", "",
+             "Command (from the repository root):", "", "    " + PROFILE_CMDS["trace"], "",
+             "| kernel | calls | avg us | min us | max us | share |", "|---|---|---|---|---|---|"]
+    for r in _csv_rows(stats[0]):
+        name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        lines.append("| %s | %s | %.3f | %.3f | %.3f | %s%% |" % (
+            name, r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
+            r["Percentage"]))
+    open(os.path.join(prof, "kernel_stats_moe_layer.md"), "w").write("\n".join(lines) + "\n")
+    cal_f, _ = _pmc_mean(glob.glob(os.path.join(out_dir, "pmc_cal_fetch", "*counter_collection.csv"))[0],
+                         "FETCH_SIZE", "k_elementwise")
+    cal_w, _ = _pmc_mean(glob.glob(os.path.join(out_dir, "pmc_cal_write", "*counter_collection.csv"))[0],
+                         "WRITE_SIZE", "k_elementwise")
+    copy_bytes = 64 * 1024 * 1024 * 4
+    f_fac, w_fac = copy_bytes / (cal_f * 1024), copy_bytes / (cal_w * 1024)
+    W, F, E, K = 2048, 512, 512, 10
+    algo = decode_kernel_bytes(W, F, E, K)
+    algo_by_kernel = {"k_decode_route": algo["decode_route"], "k_decode_gate_up": algo["decode_gate_up"],
+                      "k_decode_down": algo["decode_down_combine"]}
+    traffic, md = {}, ["# HBM traffic per launch: decode T=1 kernels (8 rotated layers)", "",
+                       "Commands (from the repository root):", ""]
+    md += ["    " + PROFILE_CMDS[k] for k in ("fetch", "write", "cal_fetch", "cal_write")]
+    md += ["", "Calibration: the copy kernel (strata_elementwise, 256 MiB read + 256 MiB written per launch) "
+           "reads FETCH_SIZE %.0f KiB and WRITE_SIZE %.0f KiB per dispatch, so FETCH_SIZE is scaled by %.3f and "
+           "WRITE_SIZE by %.3f." % (cal_f, cal_w, f_fac, w_fac), "",
+           "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes | algorithmic bytes | ratio |",
+           "|---|---|---|---|---|---|---|"]
+    for k in DECODE_KERNELS:
+        fk, n = _pmc_mean(glob.glob(os.path.join(out_dir, "pmc_fetch", "*counter_collection.csv"))[0],
+                          "FETCH_SIZE", k)
+        wk, _ = _pmc_mean(glob.glob(os.path.join(out_dir, "pmc_write", "*counter_collection.csv"))[0],
+                          "WRITE_SIZE", k)
+        if fk is None or wk is None:
+            continue
+        t = int(round(fk * 1024 * f_fac + wk * 1024 * w_fac))
+        traffic[k] = t
+        md.append("| %s | %d | %.1f | %.1f | %d | %d | %.2f |" % (k, n, fk, wk, t, algo_by_kernel[k],
+                                                                 t / algo_by_kernel[k]))
+    json.dump(traffic, open(os.path.join(prof, "traffic.json"), "w"), indent=1)
+    open(os.path.join(prof, "traffic_decode_T1.md"), "w").write("\n".join(md) + "\n")
+    print(json.dumps({"summaries": sorted(os.listdir(prof)), "traffic": traffic}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,9 +188,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="write the profiles/ summaries from rocprofv3 CSVs under DIR (no GPU needed)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run the copy kernel used to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.summarize:
+        return summarize(args.summarize)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the MoE layer on a single MI355X (no multi-GPU path); "
               "use --gpus 1", file=sys.stderr)
