@@ -63,7 +63,7 @@ def build_addon():
     tmp = ADDON + ".tmp"
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-DNAPI_VERSION=8", "-I/usr/include/node",
           "-I", INCLUDE, "-o", tmp, src, "-L", HERE, "-lstrata_mi355x", "-Wl,-rpath,$ORIGIN/..",
-          "-Wl,--unresolved-symbols=ignore-in-shared-libs"])
+          "-DNODE_GYP_MODULE_NAME=strata_addon"])
     os.replace(tmp, ADDON)
     return ADDON
 
