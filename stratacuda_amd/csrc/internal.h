@@ -72,8 +72,15 @@ int route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t 
 // Unchecked launchers on raw device pointers (callers validated the buffers).
 int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float *Wr, const float *bias, int experts,
                  int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out);
+// M-tile bases the dispatch writes for the grouped GEMMs: segments with at
+// least `split` rows in tiles of mt_big rows (big[]), the others in tiles of
+// mt_small rows (small[]); each array has experts + 2 entries.
+struct GemmTiling {
+    int *small, *big;
+    int split, mt_small, mt_big;
+};
 int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int experts, int *offsets, int *rows, int *parts,
-                    int *where_, char *workspace, int extra_rows, int *tile_base_out);
+                    int *where_, char *workspace, int extra_rows, const GemmTiling *tiling);
 int dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets, uint64_t rows,
              uint64_t parts, uint64_t where_, uint64_t workspace, uint64_t workspace_bytes, int extra_rows);
 uint64_t dispatch_workspace(int tokens, int experts);

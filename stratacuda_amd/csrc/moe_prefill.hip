@@ -11,24 +11,34 @@
 //
 // Grouped GEMM on MFMA (v_mfma_f32_32x32x16_f16, f32 accumulation):
 //  * Weights: (code - 1) * fp16 scale is exactly representable in fp16, so the
-//    B operand holds the exact reference weights. Codes are turned into fp16
-//    pairs with one mask ((w >> 2j) & 0x00030003 puts codes j and j+8 of a
-//    16-code word into the two halves), an OR with the exponent pattern of
-//    1024 (0x6400), a packed subtract of 1025 and a packed multiply by the
-//    group scale; all three steps are exact.
-//  * Activations: x is split into hi = fp16(x) and lo = fp16(x - hi); two
-//    MFMAs (hi and lo) per K step give products accurate to ~2^-22 relative,
-//    well inside the 1e-4 / 1e-3 output tolerance, where a single fp16 or bf16
-//    pass is not.
-//  * K order inside a 64-wide scale group is permuted identically for A and B
-//    (the dot product does not depend on it) so that both the code unpacking
-//    and the LDS reads of A are plain, conflict-free vector accesses.
-//  * Tiles: 32 rows (positions of one expert segment) x 128 weight rows per
-//    256-thread block, each wave a 32 x 32 MFMA tile; A (x hi/lo) is staged in
-//    LDS per scale group with double buffering, B is dequantised in registers.
-//    grid.x = n-block (fastest) so all m-tiles of one (expert, n-block) land
-//    on the same XCD and share its L2.
+//    B operand holds the exact reference weights. Codes become fp16 pairs with
+//    one mask ((w >> 2p) & 0x00030003 puts codes p and p+8 of a 16-code word
+//    into the two halves), an OR with the exponent pattern of 1024 (0x6400), a
+//    packed subtract of 1025 and a packed multiply by the group scale; all
+//    three steps are exact. Each wave dequantises its own B fragments in
+//    registers, once per K step, and uses each for 2 * MI MFMAs.
+//  * Activations are split once into hi = fp16(x) and lo = fp16(x - hi) (the
+//    gate/up input by k_split_hilo, the down input by the gate/up epilogue);
+//    two MFMAs (hi and lo) per K step give products accurate to ~2^-22
+//    relative, well inside the 1e-4 / 1e-3 output tolerance, where a single
+//    fp16 or bf16 pass is not. Valid for |x| < 65504.
+//  * K order: within every 64-wide scale group, position q = 16w + 2p + o
+//    holds element 16w + p + 8o. That is the order in which the pairs
+//    (p, p+8) of word w come out of the code unpacking, so B needs no
+//    shuffle; the activations are stored in the same order, so staging them
+//    into LDS is a plain 16-byte copy and the MFMA A operand one 16-byte read.
+//  * Tiles: each wave MI x NI MFMA tiles of 32 x 32. Segments of more than 32
+//    rows run in 64-row tiles with 64 x 512 blocks (8 waves of 64 x 64),
+//    shorter ones in one 32-row tile with 32 x 1024 blocks (8 waves of
+//    32 x 128), in two launches, so each activation row is read from memory
+//    once or twice per GEMM; the A tile (hi and lo) is staged in LDS per scale
+//    group, double-buffered, with the next group's A and B loads in flight
+//    during the current MFMAs.
+//    grid.x = n-block (fastest) so the m-tiles of one (expert, n-block) run
+//    on one XCD and share its L2.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "internal.h"
 #include "strata_device.h"
@@ -41,24 +51,41 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int MT = 32;   // rows (positions) per tile
-constexpr int NB = 128;  // weight rows per block (4 waves x 32)
+constexpr int APITCH = 72;  // halves per staged A row: 64 + 8 padding (LDS banks)
 
-__device__ __forceinline__ half2v codes_to_half2(uint32_t word, int jj, half2v scale) {
-    uint32_t t = ((word >> (2 * jj)) & 0x00030003u) | 0x64006400u;  // fp16 (1024 + c, 1024 + c')
+// Position of element r (0..63) of a scale group in the MFMA K order.
+__device__ __forceinline__ int k_position(int r) {
+    const int w = r >> 4, t = r & 15;
+    return 16 * w + 2 * (t & 7) + (t >> 3);
+}
+
+// X [rows x K] f32 -> hi/lo fp16 [rows][K/64][2][64] in the MFMA K order.
+__global__ void k_split_hilo(const float *__restrict__ X, _Float16 *__restrict__ out, int64_t groups) {
+    const int64_t at = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t rg = at >> 6;
+    if (rg >= groups) return;
+    const int q = (int)(at & 63), w = q >> 4, t = q & 15;
+    const float x = X[rg * 64 + 16 * w + (t >> 1) + 8 * (t & 1)];
+    const _Float16 hi = (_Float16)x;
+    out[rg * 128 + q] = hi;
+    out[rg * 128 + 64 + q] = (_Float16)(x - (float)hi);
+}
+
+__device__ __forceinline__ half2v codes_to_half2(uint32_t word, int p, half2v scale) {
+    uint32_t t = ((word >> (2 * p)) & 0x00030003u) | 0x64006400u;  // fp16 (1024 + c_p, 1024 + c_{p+8})
     half2v h = __builtin_bit_cast(half2v, t);
     const half2v k1025 = {(_Float16)1025.0f, (_Float16)1025.0f};
-    h = h - k1025;  // c - 1, exact
+    h = h - k1025;     // c - 1, exact
     return h * scale;  // (c - 1) * scale, exact in fp16
 }
 
-// B operand (8 fp16 weights) of MFMA step s from the lane's two code words.
-__device__ __forceinline__ half8 b_operand(uint32_t w0, uint32_t w1, int s, half2v scale) {
-    const uint32_t w = s < 2 ? w0 : w1;
-    const int jj0 = 4 * (s & 1);
-    half2v p0 = codes_to_half2(w, jj0 + 0, scale), p1 = codes_to_half2(w, jj0 + 1, scale);
-    half2v p2 = codes_to_half2(w, jj0 + 2, scale), p3 = codes_to_half2(w, jj0 + 3, scale);
-    half8 b = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+// B operand of K step s for lane half kh: positions 16s + 8kh .. +7, i.e. the
+// pairs (p, p+8) of word s for p = 4kh .. 4kh+3.
+__device__ __forceinline__ half8 b_operand(uint4 c, int s, int kh, half2v scale) {
+    const uint32_t w = s == 0 ? c.x : s == 1 ? c.y : s == 2 ? c.z : c.w;
+    const half2v p0 = codes_to_half2(w, 4 * kh + 0, scale), p1 = codes_to_half2(w, 4 * kh + 1, scale);
+    const half2v p2 = codes_to_half2(w, 4 * kh + 2, scale), p3 = codes_to_half2(w, 4 * kh + 3, scale);
+    const half8 b = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     return b;
 }
 
@@ -73,106 +100,368 @@ __device__ __forceinline__ int find_segment(const int *tile_base, int nseg, int 
     return lo;
 }
 
-// GATE_UP: A = X rows gathered through rows[], K = width, N = 2*ff, output H
-//          [positions x ff] = SiLU(gate) * up of interleaved column pairs.
-// else:    A = H rows by position, K = ff, N = width, output P [positions x width].
-template <bool GATE_UP>
-__global__ void __launch_bounds__(256) k_grouped_gemm(const float *__restrict__ A, const int *__restrict__ rows,
-                                                      const int *__restrict__ offsets,
-                                                      const int *__restrict__ tile_base,
-                                                      const uint8_t *__restrict__ arena, uint64_t stride,
-                                                      const uint8_t *__restrict__ shared_blob, int experts,
-                                                      uint64_t codes_off, uint64_t scales_off, int K, int N,
-                                                      float *__restrict__ out, int out_ld) {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2][2][4 * 2 * MT * 8];  // [buf][hi/lo][s][h][i][8]
+// GATE_UP: A = X (hi/lo) rows gathered through rows[], K = width, N = 2*ff;
+//          output H (hi/lo, K order) [positions][ff/64][2][64] = SiLU(gate) * up
+//          of the interleaved column pairs.
+// else:    A = H (hi/lo) rows by position, K = ff, N = width; output P f32
+//          [positions x width].
+template <bool GATE_UP, int MI, int NI, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) k_moe_gemm(const _Float16 *__restrict__ A, const int *__restrict__ rows,
+                                                  const int *__restrict__ offsets, const int *__restrict__ tiles,
+                                                  const uint8_t *__restrict__ arena, uint64_t stride,
+                                                  const uint8_t *__restrict__ shared_blob, int experts,
+                                                  uint64_t codes_off, uint64_t scales_off, int K, int N,
+                                                  void *__restrict__ out, int out_ld) {
+    constexpr int THREADS = 64 * WM * WN, BM = 32 * MI * WM, BN = 32 * NI * WN;
+    constexpr int ACH = (BM * 16 + THREADS - 1) / THREADS;  // 16-byte A chunks per thread and group
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2][2 * BM * APITCH];  // [buf][hi/lo][row][APITCH]
     const int nseg = experts + 1;
     const int tau = blockIdx.y;
-    if (tau >= tile_base[nseg]) return;
-    const int e = find_segment(tile_base, nseg, tau);
-    const int m0 = offsets[e] + (tau - tile_base[e]) * MT, mend = offsets[e + 1];
+    if (tau >= tiles[nseg]) return;
+    const int e = find_segment(tiles, nseg, tau);
+    const int m0 = offsets[e] + (tau - tiles[e]) * BM, mend = offsets[e + 1];
     const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
     const int G = K / 64;
 
-    // ---- A staging: thread -> row i = tid / 8, 8 consecutive K values 8c..8c+7
-    const int si = tid >> 3, sc = tid & 7;
-    const float *arow = nullptr;
-    if (m0 + si < mend) arow = GATE_UP ? A + (int64_t)rows[m0 + si] * K : A + (int64_t)(m0 + si) * K;
-    // LDS destinations of the 8 values (see the K permutation above).
-    const int sh = sc >> 2, ssec = sc & 1, ssw = (sc & 3) >> 1;
-    auto stage = [&](int g, int buf) {
-        float v[8];
-        if (arow) {
-            float4 a0 = *(const float4 *)(arow + g * 64 + sc * 8);
-            float4 a1 = *(const float4 *)(arow + g * 64 + sc * 8 + 4);
-            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-        } else {
+    // ---- A staging: chunk c = tid + THREADS i covers row c / 16, hi/lo
+    // (c / 8) & 1, 8 halves (c & 7) * 8 of the group.
+    const _Float16 *asrc[ACH];
+    int adst[ACH];
 #pragma unroll
-            for (int q = 0; q < 8; q++) v[q] = 0.0f;
+    for (int i = 0; i < ACH; i++) {
+        const int c = tid + THREADS * i, r = c >> 4, hl = (c >> 3) & 1, part = c & 7;
+        const int pos = m0 + r;
+        asrc[i] = nullptr;
+        adst[i] = -1;
+        if (r < BM) adst[i] = (hl * BM + r) * APITCH + part * 8;
+        if (r < BM && pos < mend) {
+            const int64_t arow = GATE_UP ? rows[pos] : pos;
+            asrc[i] = A + (arow * G * 2 + hl) * 64 + part * 8;
         }
+    }
+    uint4 areg[ACH];
+    auto load_a = [&](int g) {
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int s = 2 * ssw + (q >> 2), slot = 2 * (q & 3) + ssec;
-            const int at = ((s * 2 + sh) * MT + si) * 8 + slot;
-            _Float16 hi = (_Float16)v[q];
-            _Float16 lo = (_Float16)(v[q] - (float)hi);
-            lds[buf][0][at] = hi;
-            lds[buf][1][at] = lo;
+        for (int i = 0; i < ACH; i++)
+            areg[i] = asrc[i] ? *(const uint4 *)(asrc[i] + (int64_t)g * 128) : make_uint4(0, 0, 0, 0);
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++)
+            if (adst[i] >= 0) *(uint4 *)&lds[buf][adst[i]] = areg[i];
+    };
+
+    // ---- B: lane (j = lane % 32, kh = lane / 32), weight rows n of the NI tiles
+    const int j = lane & 31, kh = lane >> 5;
+    const int nbase = blockIdx.x * BN + wn * 32 * NI;
+    const uint8_t *brow[NI];
+    const uint8_t *bsc[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ni++) {
+        const int n = nbase + ni * 32 + j;
+        brow[ni] = blob + codes_off + (uint64_t)n * (K / 4);
+        bsc[ni] = blob + scales_off + (uint64_t)n * G * 2;
+    }
+    uint4 bc[NI], bn[NI];
+    uint32_t sc[NI], sn[NI];
+    auto load_b = [&](int g, uint4 *c, uint32_t *s) {
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            c[ni] = *(const uint4 *)(brow[ni] + (uint64_t)g * 16);
+            s[ni] = *(const uint16_t *)(bsc[ni] + g * 2);
         }
     };
 
-    // ---- B: lane (j = lane % 32, h = lane / 32), weight row n
-    const int j = lane & 31, h = lane >> 5;
-    const int n = blockIdx.x * NB + wave * 32 + j;
-    const uint8_t *brow = blob + codes_off + (uint64_t)n * (K / 4) + h * 8;
-    const uint8_t *bscale = blob + scales_off + (uint64_t)n * G * 2;
-
-    float16v acc;
+    float16v acc[MI][NI];
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+    for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
 
-    stage(0, 0);
-    uint2 cw = *(const uint2 *)(brow);
-    uint32_t sb = *(const uint16_t *)(bscale);
+    load_a(0);
+    load_b(0, bc, sc);
+    store_a(0);
+    if (G > 1) {
+        load_a(1);
+        load_b(1, bn, sn);
+    }
     __syncthreads();
     for (int g = 0; g < G; g++) {
         const int buf = g & 1;
-        uint2 cw_next = cw;
-        uint32_t sb_next = sb;
-        if (g + 1 < G) {
-            stage(g + 1, buf ^ 1);
-            cw_next = *(const uint2 *)(brow + (uint64_t)(g + 1) * 16);
-            sb_next = *(const uint16_t *)(bscale + (g + 1) * 2);
+        half2v scale[NI];
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const _Float16 s16 = __builtin_bit_cast(_Float16, (uint16_t)sc[ni]);
+            scale[ni] = (half2v){s16, s16};
         }
-        const _Float16 s16 = __builtin_bit_cast(_Float16, (uint16_t)sb);
-        const half2v scale = {s16, s16};
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            half8 b = b_operand(cw.x, cw.y, s, scale);
-            const int at = ((s * 2 + h) * MT + j) * 8;
-            half8 ahi = *(const half8 *)(&lds[buf][0][at]);
-            half8 alo = *(const half8 *)(&lds[buf][1][at]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, acc, 0, 0, 0);
+            half8 b[NI];
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++) b[ni] = b_operand(bc[ni], s, kh, scale[ni]);
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++) {
+                const int at = (wm * 32 * MI + mi * 32 + j) * APITCH + 16 * s + 8 * kh;
+                const half8 ahi = *(const half8 *)&lds[buf][at];
+                const half8 alo = *(const half8 *)&lds[buf][BM * APITCH + at];
+#pragma unroll
+                for (int ni = 0; ni < NI; ni++) {
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b[ni], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b[ni], acc[mi][ni], 0, 0, 0);
+                }
+            }
         }
-        cw = cw_next;
-        sb = sb_next;
+        if (g + 1 < G) {
+            store_a(buf ^ 1);
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++) {
+                bc[ni] = bn[ni];
+                sc[ni] = sn[ni];
+            }
+            if (g + 2 < G) {
+                load_a(g + 2);
+                load_b(g + 2, bn, sn);
+            }
+        }
         __syncthreads();
     }
 
-    // ---- epilogue: acc[v] = D[i][j], i = 8*(v/4) + 4*h + v%4
+    // ---- epilogue: acc[v] = D[i][j], i = 8*(v/4) + 4*kh + v%4 (32x32 tile)
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int i = 8 * (v >> 2) + 4 * h + (v & 3);
-        if (GATE_UP) {
-            const float other = __shfl_xor(acc[v], 1, 64);
-            if ((j & 1) == 0 && m0 + i < mend)
-                out[(int64_t)(m0 + i) * out_ld + (n >> 1)] = sm::silu(acc[v]) * other;
-        } else if (m0 + i < mend) {
-            out[(int64_t)(m0 + i) * out_ld + n] = acc[v];
+    for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int i = wm * 32 * MI + mi * 32 + 8 * (v >> 2) + 4 * kh + (v & 3), pos = m0 + i;
+                const int n = nbase + ni * 32 + j;
+                if (GATE_UP) {
+                    const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[mi][ni][v], acc[mi][ni][v]);
+                    if ((j & 1) == 0 && pos < mend) {
+                        const float h = sm::silu(acc[mi][ni][v]) * other;
+                        const int jj = n >> 1;
+                        _Float16 *dst = (_Float16 *)out + ((int64_t)pos * (out_ld / 64) + (jj >> 6)) * 128 +
+                                        k_position(jj & 63);
+                        const _Float16 hi = (_Float16)h;
+                        dst[0] = hi;
+                        dst[64] = (_Float16)(h - (float)hi);
+                    }
+                } else if (pos < mend) {
+                    ((float *)out)[(int64_t)pos * out_ld + n] = acc[mi][ni][v];
+                }
+            }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming grouped GEMM: the same tiles and arithmetic as k_moe_gemm, fed by
+// a ring of three stages (one 64-wide scale group each) filled with direct
+// global->LDS loads (global_load_lds_dwordx4: lane l of a wave writes 16 bytes
+// at the instruction's LDS base + 16 l), so two groups of A and B are in
+// flight while the current one is multiplied, without occupying registers.
+// The group count K / 64 is a template parameter, so the ring is unrolled
+// into straight-line code and the compiler's own waits match the ring's.
+// Each stage is its own __shared__ array: the compiler then tracks the
+// loads into each stage separately and the waits are the explicit vmcnt
+// below. Every thread issues the same number of loads per stage (rows past a
+// segment's end load a valid row; those results are never stored), so one
+// compile-time vmcnt covers all waves. 4 waves side by side in N: block tile
+// (32 MI) x (128 NI), wave tile (32 MI) x (32 NI). Scale planes of the block's
+// weight rows (K <= 2048) are loaded once into LDS.
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma16(const void *src, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void *)lds_base, 16, 0, 0);
+}
+// Waits until at most N vector-memory operations of this wave are pending,
+// then joins the block at a barrier. The empty asm statements with a memory
+// clobber keep the compiler from moving LDS accesses across this point (the
+// barrier intrinsic alone does not order memory operations).
+template <int N>
+__device__ __forceinline__ void ring_sync() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+constexpr int STREAM_MAX_G = 32;  // K <= 2048 for the streaming kernel
+
+// One ring stage, sized for the largest tile (64 rows x 256 weight rows).
+struct StreamStage {
+    uint4 a[64 * 16];  // [hi/lo][row][8 slots of 16 B], slot = part ^ (row & 7)
+    uint4 b[256];      // [weight row] 16 B of codes (the tail is filler for 128-wide tiles)
+};
+// The stages are separate objects at namespace scope: the compiler's wait
+// insertion then tells loads into one stage from reads of another (a stage
+// declared inside the kernel made it wait for every load before any read).
+__shared__ __attribute__((aligned(16))) StreamStage g_stage0;
+__shared__ __attribute__((aligned(16))) StreamStage g_stage1;
+__shared__ __attribute__((aligned(16))) StreamStage g_stage2;
+__shared__ __attribute__((aligned(16))) uint16_t g_stream_scale[256 * STREAM_MAX_G];
+
+template <bool GATE_UP, int MI, int NI>
+struct StreamGemm {
+    static constexpr int BM = 32 * MI, BN = 128 * NI;
+    static constexpr int ACH = BM * 16 / 256;             // A loads per thread per stage
+    static constexpr int BCH = (BN + 255) / 256;          // B loads per thread per stage
+    static constexpr int PER_STAGE = ACH + BCH;
+};
+
+template <bool GATE_UP, int MI, int NI, int KG>
+__global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restrict__ A, const int *__restrict__ rows,
+                                                         const int *__restrict__ offsets, const int *__restrict__ tiles,
+                                                         const uint8_t *__restrict__ arena, uint64_t stride,
+                                                         const uint8_t *__restrict__ shared_blob, int experts,
+                                                         uint64_t codes_off, uint64_t scales_off, int K, int N,
+                                                         void *__restrict__ out, int out_ld) {
+    using P = StreamGemm<GATE_UP, MI, NI>;
+    constexpr int BM = P::BM, BN = P::BN, ACH = P::ACH, BCH = P::BCH;
+    StreamStage &st0 = g_stage0, &st1 = g_stage1, &st2 = g_stage2;
+    uint16_t *s_scale = g_stream_scale;
+    static_assert(KG >= 1 && KG <= STREAM_MAX_G, "K / 64 groups");
+    static_assert(BM <= 64 && BN <= 256, "stage size");
+    const int nseg = experts + 1;
+    const int tau = blockIdx.y;
+    if (tau >= tiles[nseg]) return;
+    const int e = find_segment(tiles, nseg, tau);
+    const int m0 = offsets[e] + (tau - tiles[e]) * BM, mend = offsets[e + 1];
+    const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr int G = KG;  // K / 64, fixed at compile time: the ring is straight-line code
+    (void)K;
+    const int n0 = blockIdx.x * BN;
+
+    // Per-thread DMA sources. A chunk c = tid + 256 i: hi/lo c / (8 BM), row
+    // (c / 8) % BM, slot c % 8 holding part slot ^ (row & 7).
+    const _Float16 *asrc[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; i++) {
+        const int c = tid + 256 * i, hl = c / (8 * BM), r = (c >> 3) % BM, part = (c & 7) ^ (r & 7);
+        const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
+        const int64_t arow = GATE_UP ? rows[pos] : pos;
+        asrc[i] = A + (arow * G * 2 + hl) * 64 + part * 8;
+    }
+    const uint8_t *bsrc[BCH];
+#pragma unroll
+    for (int i = 0; i < BCH; i++) {
+        const int c = tid + 256 * i;
+        const int n = n0 + (c < BN ? c : c % BN);  // filler lanes reload rows of the tile
+        bsrc[i] = blob + codes_off + (uint64_t)n * (K / 4);
+    }
+    auto issue = [&](StreamStage &sg, int g) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) dma16(asrc[i] + (int64_t)g * 128, &sg.a[256 * i + 64 * wave]);
+#pragma unroll
+        for (int i = 0; i < BCH; i++) dma16(bsrc[i] + (uint64_t)g * 16, &sg.b[256 * i + 64 * wave]);
+    };
+    // Scales of the block's BN rows, all groups: row n's G halves are
+    // contiguous (G * 2 bytes); 16-byte chunks, row-major in LDS. For G < 8
+    // a chunk spans rows; the rows are consecutive, so the copy is one
+    // contiguous range either way.
+    {
+        const uint8_t *base = blob + scales_off + (uint64_t)n0 * G * 2;
+        const int chunks = BN * G * 2 / 16;
+        for (int c = tid; c < chunks; c += 256) {
+            const uint4 v = *(const uint4 *)(base + (uint64_t)c * 16);
+            *(uint4 *)((uint8_t *)s_scale + c * 16) = v;
         }
     }
+    __syncthreads();
+    issue(st0, 0);
+    issue(st1, min(1, G - 1));
+
+    const int j = lane & 31, kh = lane >> 5;
+    float16v acc[MI][NI];
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
+
+    auto compute = [&](const StreamStage &sg, int g) {
+        uint4 codes[NI];
+        half2v scale[NI];
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const int nl = wave * 32 * NI + ni * 32 + j;
+            codes[ni] = sg.b[nl];
+            const _Float16 s16 = __builtin_bit_cast(_Float16, s_scale[nl * G + g]);
+            scale[ni] = (half2v){s16, s16};
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            half8 b[NI];
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++) b[ni] = b_operand(codes[ni], s, kh, scale[ni]);
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++) {
+                const int r = mi * 32 + j, slot = (2 * s + kh) ^ (r & 7);
+                const half8 ahi = __builtin_bit_cast(half8, sg.a[r * 8 + slot]);
+                const half8 alo = __builtin_bit_cast(half8, sg.a[(BM + r) * 8 + slot]);
+#pragma unroll
+                for (int ni = 0; ni < NI; ni++) {
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b[ni], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b[ni], acc[mi][ni], 0, 0, 0);
+                }
+            }
+        }
+    };
+    // Ring: at step g the stages of groups g and g+1 have been issued; the
+    // wait leaves only the latter in flight, and the slot that step g-1
+    // consumed is refilled with group g+2. Loads past the last group repeat
+    // group G-1 (their data is never read), so every step has the same
+    // number of loads in flight and no branch separates a load from the reads
+    // that follow it.
+    constexpr int PS = P::PER_STAGE;
+#pragma unroll
+    for (int g = 0; g < G; g += 3) {
+        ring_sync<PS>();  // slot 0 holds group g
+        issue(st2, min(g + 2, G - 1));
+        compute(st0, g);
+        if (g + 1 < G) {  // slot 1 holds group g + 1
+            ring_sync<PS>();
+            issue(st0, min(g + 3, G - 1));
+            compute(st1, g + 1);
+        }
+        if (g + 2 < G) {  // slot 2 holds group g + 2
+            ring_sync<PS>();
+            issue(st1, min(g + 4, G - 1));
+            compute(st2, g + 2);
+        }
+    }
+    // No load may still be writing LDS when the block ends.
+    ring_sync<0>();
+
+    // ---- epilogue: acc[v] = D[i][j], i = 8*(v/4) + 4*kh + v%4 (32x32 tile)
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int i = mi * 32 + 8 * (v >> 2) + 4 * kh + (v & 3), pos = m0 + i;
+                const int n = n0 + wave * 32 * NI + ni * 32 + j;
+                if (GATE_UP) {
+                    const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[mi][ni][v], acc[mi][ni][v]);
+                    if ((j & 1) == 0 && pos < mend) {
+                        const float h = sm::silu(acc[mi][ni][v]) * other;
+                        const int jj = n >> 1;
+                        _Float16 *dst = (_Float16 *)out + ((int64_t)pos * (out_ld / 64) + (jj >> 6)) * 128 +
+                                        k_position(jj & 63);
+                        const _Float16 hi = (_Float16)h;
+                        dst[0] = hi;
+                        dst[64] = (_Float16)(h - (float)hi);
+                    }
+                } else if (pos < mend) {
+                    ((float *)out)[(int64_t)pos * out_ld + n] = acc[mi][ni][v];
+                }
+            }
 }
 
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
@@ -197,7 +486,7 @@ constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct PrefillWs {
-    uint64_t logits, gate, dispatch, offsets, tile_base, rows, parts, where_, H, P, end;
+    uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, rows, parts, where_, Xhl, Hhl, P, end;
 };
 PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
     const uint64_t n = (uint64_t)tokens * topk, m = n + tokens;
@@ -206,12 +495,14 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
     w.gate = up(w.logits + (uint64_t)tokens * experts * 4);
     w.dispatch = up(w.gate + (uint64_t)tokens * 4);
     w.offsets = up(w.dispatch + dispatch_workspace(tokens, experts));
-    w.tile_base = up(w.offsets + ((uint64_t)experts + 2) * 4);
-    w.rows = up(w.tile_base + ((uint64_t)experts + 2) * 4);
+    w.tiles_small = up(w.offsets + ((uint64_t)experts + 2) * 4);
+    w.tiles_big = up(w.tiles_small + ((uint64_t)experts + 2) * 4);
+    w.rows = up(w.tiles_big + ((uint64_t)experts + 2) * 4);
     w.parts = up(w.rows + m * 4);
     w.where_ = up(w.parts + m * 4);
-    w.H = up(w.where_ + n * 4);
-    w.P = up(w.H + m * ff * 4);
+    w.Xhl = up(w.where_ + n * 4);
+    w.Hhl = up(w.Xhl + (uint64_t)tokens * width * 4);
+    w.P = up(w.Hhl + m * ff * 4);
     w.end = up(w.P + m * width * 4);
     return w;
 }
@@ -231,34 +522,74 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     PrefillWs w = prefill_ws(tokens, width, ff, experts, topk);
     char *ws = (char *)workspace;
     BlobLayout L = blob_layout(width, ff);
-    if ((2 * ff) % NB || width % NB)
+    if ((2 * ff) % 128 || width % 128)
         return fail(ctx, SM_E_ARG, "prefill needs width and 2*ff to be multiples of 128");
     if (int rc = stage_mark(ctx, kStagePrefillRoute)) return rc;
     if (int rc = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts,
                               topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
                               (float *)(ws + w.gate)))
         return rc;
-    int *offsets = (int *)(ws + w.offsets), *tile_base = (int *)(ws + w.tile_base);
+    int *offsets = (int *)(ws + w.offsets);
+    int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);
     if (int rc = stage_mark(ctx, kStagePrefillDispatch)) return rc;
+    const GemmTiling tiling = {tiles_small, tiles_big, 33, 32, 64};
     if (int rc = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
-                                 (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, tile_base))
+                                 (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, &tiling))
         return rc;
+    const int64_t groups = (int64_t)tokens * (width / 64);
+    k_split_hilo<<<(unsigned)((groups * 64 + 255) / 256), 256, 0, ctx->stream>>>((const float *)X,
+                                                                               (_Float16 *)(ws + w.Xhl), groups);
+    if (int rc = launched(ctx)) return rc;
     const uint64_t m = (uint64_t)tokens * topk + tokens;
-    const unsigned max_tiles = (unsigned)(m / MT + (uint64_t)experts + 2);
-    dim3 g1((unsigned)(2 * ff / NB), max_tiles);
+    const uint64_t segs = (uint64_t)experts + 1;
+    // Segment tilings: > 32 rows in 64-row tiles ("big"), <= 32 rows in one
+    // 32-row tile ("small"). Wide blocks (big 64 x 512, small 32 x 1024, 8
+    // waves) read each activation row once or twice; shapes whose N is not a
+    // multiple of those widths use 4-wave 64 x 128 / 32 x 128 blocks.
+    const unsigned big_tiles = (unsigned)(m / 64 + std::min(segs, m / 33) + 1);
+    const unsigned small_tiles = (unsigned)(segs + 1);
+    const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
+    const int *rows = (const int *)(ws + w.rows);
+    const uint8_t *ar = (const uint8_t *)arena, *sh = (const uint8_t *)shared_blob;
+    auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
+                     void *out, int ld) -> int {
+        if (N % 256 == 0 && (K == 2048 || K == 512)) {
+            auto kb = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 2, 2, 32> : k_moe_gemm_stream<true, 2, 2, 8>)
+                              : (K == 2048 ? k_moe_gemm_stream<false, 2, 2, 32> : k_moe_gemm_stream<false, 2, 2, 8>);
+            kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->stream>>>(a, r, offsets, tiles_big, ar, blob_stride,
+                                                                             sh, experts, codes, scales, K, N, out, ld);
+            if (int rc = launched(ctx)) return rc;
+            auto ks = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 1, 2, 32> : k_moe_gemm_stream<true, 1, 2, 8>)
+                              : (K == 2048 ? k_moe_gemm_stream<false, 1, 2, 32> : k_moe_gemm_stream<false, 1, 2, 8>);
+            ks<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
+                a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+            return launched(ctx);
+        }
+        if (N % 512 == 0) {
+            auto kb = gate_up ? k_moe_gemm<true, 2, 2, 1, 8> : k_moe_gemm<false, 2, 2, 1, 8>;
+            kb<<<dim3((unsigned)(N / 512), big_tiles), 512, 0, ctx->stream>>>(a, r, offsets, tiles_big, ar, blob_stride,
+                                                                             sh, experts, codes, scales, K, N, out, ld);
+        } else {
+            auto kb = gate_up ? k_moe_gemm<true, 1, 2, 2, 2> : k_moe_gemm<false, 1, 2, 2, 2>;
+            kb<<<dim3((unsigned)(N / 128), big_tiles), 256, 0, ctx->stream>>>(a, r, offsets, tiles_big, ar, blob_stride,
+                                                                             sh, experts, codes, scales, K, N, out, ld);
+        }
+        if (int rc = launched(ctx)) return rc;
+        if (N % 1024 == 0) {
+            auto ks = gate_up ? k_moe_gemm<true, 1, 4, 1, 8> : k_moe_gemm<false, 1, 4, 1, 8>;
+            ks<<<dim3((unsigned)(N / 1024), small_tiles), 512, 0, ctx->stream>>>(
+                a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+        } else {
+            auto ks = gate_up ? k_moe_gemm<true, 1, 1, 1, 4> : k_moe_gemm<false, 1, 1, 1, 4>;
+            ks<<<dim3((unsigned)(N / 128), small_tiles), 256, 0, ctx->stream>>>(
+                a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+        }
+        return launched(ctx);
+    };
     if (int rc = stage_mark(ctx, kStagePrefillGateUp)) return rc;
-    k_grouped_gemm<true><<<g1, 256, 0, ctx->stream>>>((const float *)X, (const int *)(ws + w.rows), offsets, tile_base,
-                                                      (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob,
-                                                      experts, L.gate_up_codes, L.gate_up_scales, width, 2 * ff,
-                                                      (float *)(ws + w.H), ff);
-    if (int rc = launched(ctx)) return rc;
-    dim3 g2((unsigned)(width / NB), max_tiles);
+    if (int rc = gemms(true, xhl, rows, width, 2 * ff, L.gate_up_codes, L.gate_up_scales, ws + w.Hhl, ff)) return rc;
     if (int rc = stage_mark(ctx, kStagePrefillDown)) return rc;
-    k_grouped_gemm<false><<<g2, 256, 0, ctx->stream>>>((const float *)(ws + w.H), nullptr, offsets, tile_base,
-                                                       (const uint8_t *)arena, blob_stride,
-                                                       (const uint8_t *)shared_blob, experts, L.down_codes,
-                                                       L.down_scales, ff, width, (float *)(ws + w.P), width);
-    if (int rc = launched(ctx)) return rc;
+    if (int rc = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return rc;
     const uint64_t total = (uint64_t)tokens * width;
     if (int rc = stage_mark(ctx, kStagePrefillCombine)) return rc;
     k_combine<<<(unsigned)((total + 255) / 256), 256, 0, ctx->stream>>>(

@@ -170,13 +170,16 @@ __global__ void __launch_bounds__(256) k_dispatch_masks(const int *__restrict__ 
 
 // Single block: exclusive scan of counts (expert-major) into base, per-expert
 // offsets[E+1] (+ offsets[E+1] = offsets[E] + extra for the shared-expert
-// segment), and m-tile bases for the grouped GEMMs: tile_base[s] = sum over
-// segments s' < s of ceil(n_s' / mt) (segments = experts, then the extra one).
+// segment), and the m-tile bases of the grouped GEMMs over the E+1 segments:
+// a segment with at least `split` rows is tiled by mt_big rows in tile_big
+// and is absent from tile_small, a shorter one the other way round
+// (tile_x[s] = tiles of the segments before s; tile_x[E+1] = the total).
 __global__ void __launch_bounds__(1024) k_dispatch_scan(const int *__restrict__ counts, int *__restrict__ base,
-                                                        int *__restrict__ offsets, int *__restrict__ tile_base,
-                                                        int experts, int nb, int extra, int mt) {
+                                                        int *__restrict__ offsets, int *__restrict__ tile_small,
+                                                        int *__restrict__ tile_big, int experts, int nb, int extra,
+                                                        int split, int mt_small, int mt_big) {
     __shared__ int part[1024];
-    __shared__ int seg[513];
+    __shared__ int tsm[1024], tbg[1024];
     const int n = experts * nb, tid = threadIdx.x;
     const int chunk = (n + 1023) / 1024, lo = min(n, tid * chunk), hi = min(n, lo + chunk);
     int s = 0;
@@ -202,19 +205,27 @@ __global__ void __launch_bounds__(1024) k_dispatch_scan(const int *__restrict__ 
         offsets[experts + 1] = total + extra;
     }
     __syncthreads();
-    // Tile bases over experts + 1 segments (the last may be empty).
-    for (int e = tid; e <= experts; e += 1024) {
-        int cnt = offsets[e + 1] - offsets[e];
-        seg[e] = (cnt + mt - 1) / mt;
+    // Tiles per segment (experts + 1 segments, the last may be empty), then an
+    // inclusive scan of each kind; experts + 1 <= 513 < 1024.
+    int ns = 0, nbg = 0;
+    if (tid <= experts) {
+        const int cnt = offsets[tid + 1] - offsets[tid];
+        if (cnt >= split) nbg = (cnt + mt_big - 1) / mt_big;
+        else ns = (cnt + mt_small - 1) / mt_small;
     }
+    tsm[tid] = ns;
+    tbg[tid] = nbg;
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int e = 0; e <= experts; e++) {
-            tile_base[e] = acc;
-            acc += seg[e];
-        }
-        tile_base[experts + 1] = acc;
+    for (int d = 1; d < 1024; d <<= 1) {
+        int vs = tid >= d ? tsm[tid - d] : 0, vb = tid >= d ? tbg[tid - d] : 0;
+        __syncthreads();
+        tsm[tid] += vs;
+        tbg[tid] += vb;
+        __syncthreads();
+    }
+    if (tid <= experts + 1) {
+        if (tile_small) tile_small[tid] = tid ? tsm[tid - 1] : 0;
+        if (tile_big) tile_big[tid] = tid ? tbg[tid - 1] : 0;
     }
 }
 
@@ -246,11 +257,10 @@ __global__ void k_dispatch_place(const int *__restrict__ ids, int tokens, int to
 
 // ---------------------------------------------------------- workspace
 constexpr uint64_t kAlign = 256;
-constexpr int kGemmMT = 32;  // token rows per grouped-GEMM tile (moe_prefill.hip)
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct DispatchWs {
-    uint64_t status, masks, counts, base, tile_base, end;
+    uint64_t status, masks, counts, base, tile_small, tile_big, end;
 };
 DispatchWs dispatch_ws(int tokens, int experts) {
     const uint64_t nb = (uint64_t)(tokens + 63) / 64;
@@ -259,8 +269,9 @@ DispatchWs dispatch_ws(int tokens, int experts) {
     w.masks = up(w.status + 64);
     w.counts = up(w.masks + nb * experts * 8);
     w.base = up(w.counts + nb * experts * 4);
-    w.tile_base = up(w.base + nb * experts * 4);
-    w.end = up(w.tile_base + ((uint64_t)experts + 2) * 4);
+    w.tile_small = up(w.base + nb * experts * 4);
+    w.tile_big = up(w.tile_small + ((uint64_t)experts + 2) * 4);
+    w.end = up(w.tile_big + ((uint64_t)experts + 2) * 4);
     return w;
 }
 
@@ -321,7 +332,7 @@ int route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t 
 }
 
 int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int experts, int *offsets, int *rows, int *parts,
-                    int *where_, char *ws, int extra_rows, int *tile_base_out) {
+                    int *where_, char *ws, int extra_rows, const GemmTiling *tiling) {
     const int nb = ceil_div(tokens, 64);
     DispatchWs w = dispatch_ws(tokens, experts);
     const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
@@ -329,9 +340,11 @@ int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int exper
     k_dispatch_masks<<<nb, 256, 0, ctx->stream>>>(ids, tokens, topk, experts, nb, (unsigned long long *)(ws + w.masks),
                                                   (int *)(ws + w.counts), (uint32_t *)(ws + w.status));
     if (int rc = launched(ctx)) return rc;
-    int *tile_base = tile_base_out ? tile_base_out : (int *)(ws + w.tile_base);
-    k_dispatch_scan<<<1, 1024, 0, ctx->stream>>>((const int *)(ws + w.counts), (int *)(ws + w.base), offsets, tile_base,
-                                                 experts, nb, (int)extra, kGemmMT);
+    GemmTiling none = {(int *)(ws + w.tile_small), (int *)(ws + w.tile_big), 64, 32, 128};
+    const GemmTiling &tl = tiling ? *tiling : none;
+    k_dispatch_scan<<<1, 1024, 0, ctx->stream>>>((const int *)(ws + w.counts), (int *)(ws + w.base), offsets,
+                                                 tl.small, tl.big, experts, nb, (int)extra, tl.split, tl.mt_small,
+                                                 tl.mt_big);
     if (int rc = launched(ctx)) return rc;
     const uint64_t threads = n + extra;
     k_dispatch_place<<<(unsigned)((threads + 255) / 256), 256, 0, ctx->stream>>>(
