@@ -71,6 +71,14 @@ __global__ void k_split_hilo(const float *__restrict__ X, _Float16 *__restrict__
     out[rg * 128 + 64 + q] = (_Float16)(x - (float)hi);
 }
 
+// SiLU for the fused prefill epilogue, whose outputs are checked to a
+// tolerance (1e-4 + 1e-3 |e|): exp through the hardware v_exp_f32 (2^x) and a
+// hardware reciprocal, a few ulp from the libm form.
+__device__ __forceinline__ float silu_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 __device__ __forceinline__ half2v codes_to_half2(uint32_t word, int p, half2v scale) {
     uint32_t t = ((word >> (2 * p)) & 0x00030003u) | 0x64006400u;  // fp16 (1024 + c_p, 1024 + c_{p+8})
     half2v h = __builtin_bit_cast(half2v, t);
@@ -242,7 +250,7 @@ __global__ void __launch_bounds__(64 * WM * WN) k_moe_gemm(const _Float16 *__res
                 if (GATE_UP) {
                     const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[mi][ni][v], acc[mi][ni][v]);
                     if ((j & 1) == 0 && pos < mend) {
-                        const float h = sm::silu(acc[mi][ni][v]) * other;
+                        const float h = silu_fast(acc[mi][ni][v]) * other;
                         const int jj = n >> 1;
                         _Float16 *dst = (_Float16 *)out + ((int64_t)pos * (out_ld / 64) + (jj >> 6)) * 128 +
                                         k_position(jj & 63);
@@ -291,18 +299,51 @@ __device__ __forceinline__ void ring_sync() {
 
 constexpr int STREAM_MAX_G = 32;  // K <= 2048 for the streaming kernel
 
-// One ring stage, sized for the largest tile (64 rows x 256 weight rows).
-struct StreamStage {
-    uint4 a[64 * 16];  // [hi/lo][row][8 slots of 16 B], slot = part ^ (row & 7)
-    uint4 b[256];      // [weight row] 16 B of codes (the tail is filler for 128-wide tiles)
+// Ring stages. Each stage is a separate object at namespace scope: the
+// compiler's wait insertion then tells loads into one stage from reads of
+// another (stages declared inside the kernel made it wait for every load
+// before any read). Big tiles (64 x 256) use three stages, small tiles
+// (32 x 256) five; the scale planes of the block's weight rows sit beside.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+template <int BM>
+struct RingStage {
+    v4u a[BM * 16];  // [hi/lo][row][8 slots of 16 B], slot = part ^ ((row >> 1) & 7)
+    v4u b[256];      // [weight row] 16 B of codes (the tail is filler for 128-wide tiles)
 };
-// The stages are separate objects at namespace scope: the compiler's wait
-// insertion then tells loads into one stage from reads of another (a stage
-// declared inside the kernel made it wait for every load before any read).
-__shared__ __attribute__((aligned(16))) StreamStage g_stage0;
-__shared__ __attribute__((aligned(16))) StreamStage g_stage1;
-__shared__ __attribute__((aligned(16))) StreamStage g_stage2;
+__shared__ __attribute__((aligned(16))) RingStage<64> g_big0, g_big1, g_big2;
+__shared__ __attribute__((aligned(16))) RingStage<32> g_small0, g_small1, g_small2, g_small3, g_small4;
 __shared__ __attribute__((aligned(16))) uint16_t g_stream_scale[256 * STREAM_MAX_G];
+
+template <int BM>
+struct Ring;
+template <>
+struct Ring<64> {
+    static constexpr int NS = 3;
+    template <int S>
+    static __device__ __forceinline__ RingStage<64> &stage() {
+        return S == 0 ? g_big0 : S == 1 ? g_big1 : g_big2;
+    }
+};
+template <>
+struct Ring<32> {
+    static constexpr int NS = 5;
+    template <int S>
+    static __device__ __forceinline__ RingStage<32> &stage() {
+        return S == 0 ? g_small0 : S == 1 ? g_small1 : S == 2 ? g_small2 : S == 3 ? g_small3 : g_small4;
+    }
+};
+// Calls f(stage S) for the S equal to `slot` (slot is a constant once the
+// group loop is unrolled).
+template <int BM, typename F>
+__device__ __forceinline__ void with_stage(int slot, F &&f) {
+    switch (slot) {
+    case 0: f(Ring<BM>::template stage<0>()); break;
+    case 1: f(Ring<BM>::template stage<1 % Ring<BM>::NS>()); break;
+    case 2: f(Ring<BM>::template stage<2 % Ring<BM>::NS>()); break;
+    case 3: f(Ring<BM>::template stage<3 % Ring<BM>::NS>()); break;
+    default: f(Ring<BM>::template stage<4 % Ring<BM>::NS>()); break;
+    }
+}
 
 template <bool GATE_UP, int MI, int NI>
 struct StreamGemm {
@@ -321,7 +362,8 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
                                                          void *__restrict__ out, int out_ld) {
     using P = StreamGemm<GATE_UP, MI, NI>;
     constexpr int BM = P::BM, BN = P::BN, ACH = P::ACH, BCH = P::BCH;
-    StreamStage &st0 = g_stage0, &st1 = g_stage1, &st2 = g_stage2;
+    using Stage = RingStage<BM>;
+    constexpr int NS = Ring<BM>::NS;
     uint16_t *s_scale = g_stream_scale;
     static_assert(KG >= 1 && KG <= STREAM_MAX_G, "K / 64 groups");
     static_assert(BM <= 64 && BN <= 256, "stage size");
@@ -337,11 +379,13 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     const int n0 = blockIdx.x * BN;
 
     // Per-thread DMA sources. A chunk c = tid + 256 i: hi/lo c / (8 BM), row
-    // (c / 8) % BM, slot c % 8 holding part slot ^ (row & 7).
+    // (c / 8) % BM, slot c % 8 holding part slot ^ ((row / 2) & 7). A 128-bit
+    // LDS read serves 16 lanes per pass; the 16 rows a pass reads (one part
+    // each) then fall on 16 distinct 16-byte bank groups.
     const _Float16 *asrc[ACH];
 #pragma unroll
     for (int i = 0; i < ACH; i++) {
-        const int c = tid + 256 * i, hl = c / (8 * BM), r = (c >> 3) % BM, part = (c & 7) ^ (r & 7);
+        const int c = tid + 256 * i, hl = c / (8 * BM), r = (c >> 3) % BM, part = (c & 7) ^ ((r >> 1) & 7);
         const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
         const int64_t arow = GATE_UP ? rows[pos] : pos;
         asrc[i] = A + (arow * G * 2 + hl) * 64 + part * 8;
@@ -353,27 +397,32 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
         const int n = n0 + (c < BN ? c : c % BN);  // filler lanes reload rows of the tile
         bsrc[i] = blob + codes_off + (uint64_t)n * (K / 4);
     }
-    auto issue = [&](StreamStage &sg, int g) {
+    auto issue = [&](Stage &sg, int g) {
 #pragma unroll
         for (int i = 0; i < ACH; i++) dma16(asrc[i] + (int64_t)g * 128, &sg.a[256 * i + 64 * wave]);
 #pragma unroll
         for (int i = 0; i < BCH; i++) dma16(bsrc[i] + (uint64_t)g * 16, &sg.b[256 * i + 64 * wave]);
     };
-    // Scales of the block's BN rows, all groups: row n's G halves are
-    // contiguous (G * 2 bytes); 16-byte chunks, row-major in LDS. For G < 8
-    // a chunk spans rows; the rows are consecutive, so the copy is one
-    // contiguous range either way.
+    // Scales of the block's BN rows, all groups, stored [group][row] in LDS so
+    // that the lanes of a wave read consecutive halves. The plane is
+    // [row][G] in memory: read as 16-byte chunks (8 consecutive scales of
+    // the flattened range, possibly spanning rows), written out by element.
     {
         const uint8_t *base = blob + scales_off + (uint64_t)n0 * G * 2;
         const int chunks = BN * G * 2 / 16;
         for (int c = tid; c < chunks; c += 256) {
             const uint4 v = *(const uint4 *)(base + (uint64_t)c * 16);
-            *(uint4 *)((uint8_t *)s_scale + c * 16) = v;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int flat = c * 8 + q, row = flat / G, grp = flat - row * G;
+                s_scale[grp * BN + row] = (uint16_t)(w[q >> 1] >> (16 * (q & 1)));
+            }
         }
     }
     __syncthreads();
-    issue(st0, 0);
-    issue(st1, min(1, G - 1));
+#pragma clang loop unroll(full)
+    for (int q = 0; q < NS - 1; q++) with_stage<BM>(q, [&](Stage &sg) { issue(sg, min(q, G - 1)); });
 
     const int j = lane & 31, kh = lane >> 5;
     float16v acc[MI][NI];
@@ -384,14 +433,15 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
 
-    auto compute = [&](const StreamStage &sg, int g) {
+    auto compute = [&](const Stage &sg, int g) {
         uint4 codes[NI];
         half2v scale[NI];
 #pragma unroll
         for (int ni = 0; ni < NI; ni++) {
             const int nl = wave * 32 * NI + ni * 32 + j;
-            codes[ni] = sg.b[nl];
-            const _Float16 s16 = __builtin_bit_cast(_Float16, s_scale[nl * G + g]);
+            const v4u cv = sg.b[nl];
+            codes[ni] = make_uint4(cv.x, cv.y, cv.z, cv.w);
+            const _Float16 s16 = __builtin_bit_cast(_Float16, s_scale[g * BN + nl]);
             scale[ni] = (half2v){s16, s16};
         }
 #pragma unroll
@@ -401,7 +451,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
             for (int ni = 0; ni < NI; ni++) b[ni] = b_operand(codes[ni], s, kh, scale[ni]);
 #pragma unroll
             for (int mi = 0; mi < MI; mi++) {
-                const int r = mi * 32 + j, slot = (2 * s + kh) ^ (r & 7);
+                const int r = mi * 32 + j, slot = (2 * s + kh) ^ ((r >> 1) & 7);
                 const half8 ahi = __builtin_bit_cast(half8, sg.a[r * 8 + slot]);
                 const half8 alo = __builtin_bit_cast(half8, sg.a[(BM + r) * 8 + slot]);
 #pragma unroll
@@ -412,28 +462,18 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
             }
         }
     };
-    // Ring: at step g the stages of groups g and g+1 have been issued; the
-    // wait leaves only the latter in flight, and the slot that step g-1
-    // consumed is refilled with group g+2. Loads past the last group repeat
-    // group G-1 (their data is never read), so every step has the same
-    // number of loads in flight and no branch separates a load from the reads
-    // that follow it.
+    // Ring of NS stages: before step g the groups up to g + NS - 2 have been
+    // issued; the wait leaves the NS - 2 after g in flight, and the slot
+    // that step g-1 consumed is refilled with group g + NS - 1. Loads past the
+    // last group repeat group G-1 (their data is never read), so every step
+    // has the same number of loads in flight and no branch separates a load
+    // from the reads that follow it.
     constexpr int PS = P::PER_STAGE;
-#pragma unroll
-    for (int g = 0; g < G; g += 3) {
-        ring_sync<PS>();  // slot 0 holds group g
-        issue(st2, min(g + 2, G - 1));
-        compute(st0, g);
-        if (g + 1 < G) {  // slot 1 holds group g + 1
-            ring_sync<PS>();
-            issue(st0, min(g + 3, G - 1));
-            compute(st1, g + 1);
-        }
-        if (g + 2 < G) {  // slot 2 holds group g + 2
-            ring_sync<PS>();
-            issue(st1, min(g + 4, G - 1));
-            compute(st2, g + 2);
-        }
+#pragma clang loop unroll(full)
+    for (int g = 0; g < G; g++) {
+        ring_sync<PS * (NS - 2)>();
+        with_stage<BM>((g + NS - 1) % NS, [&](Stage &sg) { issue(sg, min(g + NS - 1, G - 1)); });
+        with_stage<BM>(g % NS, [&](Stage &sg) { compute(sg, g); });
     }
     // No load may still be writing LDS when the block ends.
     ring_sync<0>();
@@ -450,7 +490,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
                 if (GATE_UP) {
                     const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[mi][ni][v], acc[mi][ni][v]);
                     if ((j & 1) == 0 && pos < mend) {
-                        const float h = sm::silu(acc[mi][ni][v]) * other;
+                        const float h = silu_fast(acc[mi][ni][v]) * other;
                         const int jj = n >> 1;
                         _Float16 *dst = (_Float16 *)out + ((int64_t)pos * (out_ld / 64) + (jj >> 6)) * 128 +
                                         k_position(jj & 63);
@@ -465,21 +505,42 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
 }
 
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
-__global__ void k_combine(const float *__restrict__ P, const int *__restrict__ where_,
-                          const float *__restrict__ weights, const float *__restrict__ gate,
-                          const int *__restrict__ offsets, float *__restrict__ Y, int tokens, int topk, int width,
-                          int experts) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)tokens * width) return;
-    const int t = (int)(i / width), d = (int)(i % width);
-    const int64_t sb = offsets[experts];
-    float value = P[(sb + t) * width + d] * sm::sigmoid(gate[t]);
-    for (int k = 0; k < topk; k++) {
-        const int pos = where_[(int64_t)t * topk + k];
-        const float part = pos >= 0 ? P[(int64_t)pos * width + d] : __builtin_nanf("");
-        value = value + part * weights[(int64_t)t * topk + k];
+// in the reference order (kernels/strata.cu:470-476). One block per token:
+// the token's slot positions, weights and sigmoid(gate) are read once, then
+// each thread combines 4 consecutive outputs per step with 16-byte loads.
+// Needs width % 4 == 0.
+constexpr int COMBINE_MAX_K = 32;
+__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, const int *__restrict__ where_,
+                                                 const float *__restrict__ weights, const float *__restrict__ gate,
+                                                 const int *__restrict__ offsets, float *__restrict__ Y, int tokens,
+                                                 int topk, int width, int experts) {
+    __shared__ int s_pos[COMBINE_MAX_K];
+    __shared__ float s_w[COMBINE_MAX_K];
+    __shared__ float s_sig;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (tid < topk) {
+        s_pos[tid] = where_[(int64_t)t * topk + tid];
+        s_w[tid] = weights[(int64_t)t * topk + tid];
     }
-    Y[i] = value;
+    if (tid == 0) s_sig = sm::sigmoid(gate[t]);
+    __syncthreads();
+    const float sig = s_sig;
+    const float4 *shared_row = (const float4 *)(P + ((int64_t)offsets[experts] + t) * width);
+    for (int d4 = tid; d4 < width / 4; d4 += blockDim.x) {
+        const float4 s = shared_row[d4];
+        float4 v = {s.x * sig, s.y * sig, s.z * sig, s.w * sig};
+        for (int k = 0; k < topk; k++) {
+            const int pos = s_pos[k];
+            const float w = s_w[k];
+            float4 part = {__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+            if (pos >= 0) part = ((const float4 *)(P + (int64_t)pos * width))[d4];
+            v.x = v.x + part.x * w;
+            v.y = v.y + part.y * w;
+            v.z = v.z + part.z * w;
+            v.w = v.w + part.w * w;
+        }
+        ((float4 *)(Y + (int64_t)t * width))[d4] = v;
+    }
 }
 
 constexpr uint64_t kAlign = 256;
@@ -592,7 +653,8 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     if (int rc = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return rc;
     const uint64_t total = (uint64_t)tokens * width;
     if (int rc = stage_mark(ctx, kStagePrefillCombine)) return rc;
-    k_combine<<<(unsigned)((total + 255) / 256), 256, 0, ctx->stream>>>(
+    (void)total;
+    k_combine<<<(unsigned)tokens, 256, 0, ctx->stream>>>(
         (const float *)(ws + w.P), (const int *)(ws + w.where_), (const float *)weights, (const float *)(ws + w.gate),
         offsets, (float *)Y, tokens, topk, width, experts);
     if (int rc = launched(ctx)) return rc;

@@ -183,7 +183,13 @@ __global__ void __launch_bounds__(1024) k_dispatch_scan(const int *__restrict__ 
     const int n = experts * nb, tid = threadIdx.x;
     const int chunk = (n + 1023) / 1024, lo = min(n, tid * chunk), hi = min(n, lo + chunk);
     int s = 0;
-    for (int i = lo; i < hi; i++) s += counts[i];
+    for (int b0 = lo; b0 < hi; b0 += 8) {  // 8 loads in flight at a time
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = b0 + u < hi ? counts[b0 + u] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) s += v[u];
+    }
     part[tid] = s;
     __syncthreads();
     for (int d = 1; d < 1024; d <<= 1) {
@@ -193,9 +199,15 @@ __global__ void __launch_bounds__(1024) k_dispatch_scan(const int *__restrict__ 
         __syncthreads();
     }
     int run = tid ? part[tid - 1] : 0;
-    for (int i = lo; i < hi; i++) {
-        base[i] = run;
-        run += counts[i];
+    for (int b0 = lo; b0 < hi; b0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = b0 + u < hi ? counts[b0 + u] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (b0 + u < hi) base[b0 + u] = run;
+            run += v[u];
+        }
     }
     __syncthreads();
     const int total = part[1023];
