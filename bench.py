@@ -21,7 +21,8 @@ read from profiles/traffic.json when present.
 
 prefill: T=512 (uniform routing) and T=2048 (Zipf(1.1) router prior) through
 the grouped-MFMA path, per-stage times from events, reported beside the main
-line. cpu_baseline: the CPU oracle (a restatement of the reference kernels in
+line. stack: the 48 resident layers chained (RMSNorm, MoE layer, residual) for
+128 steps at batch 1 and batch 32, one HIP graph per step. cpu_baseline: the CPU oracle (a restatement of the reference kernels in
 their operation order, OpenMP over workgroups) on the host cores, T=1 decode
 of a bounded token sample of the same layer.
 """
@@ -185,6 +186,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=96)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack runs")
+    ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--prefill-reps", type=int, default=10)
@@ -364,6 +367,43 @@ def main():
                 "dtype": "f32 in/out; experts on fp16 MFMA (exact fp16 weights, activations split hi+lo), f32 accumulate",
             }
 
+    # ---- config 5: the 48-layer stack, token by token (batch 1) and batch 32
+    stack = None
+    if not args.no_stack:
+        stack = {}
+        blob = 2 * F * W // 4 + W * F // 4 + 2 * F * (W // 64) * 2 + W * (F // 64) * 2
+        for T in (1, 32):
+            st = wl.DeviceStack(be, layers=layers, tokens=T, trace=True)
+            S = args.stack_steps
+            inputs = be.alloc(S * T * W, zero=False)
+            be.synth_normal(inputs, S * T * W, wl.BASE_SEED + 31 * T, wl.STREAM_INPUT, 1.0)
+            be.graph_begin()
+            st.step()
+            gid = be.graph_end()
+            for s in range(2):
+                be.copy(inputs, st.H[0], T * W, s * T * W, 0)
+                be.graph_launch(gid)
+            be.sync()
+            be.event_record(6)
+            for s in range(S):
+                be.copy(inputs, st.H[0], T * W, s * T * W, 0)
+                be.graph_launch(gid)
+            be.event_record(7)
+            be.sync()
+            ms = be.event_elapsed_ms(6, 7) / S
+            distinct = [len(np.unique(be.read(st.ids[l]))) for l in range(st.L)]
+            step_bytes = sum(d * blob + blob + E * W * 4 + 3 * W * 4 + 4 * T * W * 4 for d in distinct)
+            stack["batch%d" % T] = {
+                "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_step": round(ms, 4), "layers": st.L,
+                "steps": S, "distinct_experts_per_layer": round(sum(distinct) / len(distinct), 1),
+                "hbm": {"bytes_per_step": step_bytes, "achieved_GBs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                        "frac": round(step_bytes / (ms * 1e-3) / PEAK_HBM, 4)},
+                "execution": "one HIP graph per step: per layer RMSNorm, MoE layer, residual add",
+            }
+            be.graph_free(gid)
+            be.free(inputs)
+            st.free()
+
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -391,6 +431,7 @@ def main():
         "layer_roofline": layer_roof,
         "kernels": kernels,
         "prefill": prefill,
+        "stack": stack,
     }
     print(json.dumps(out))
     be.dispose()

@@ -116,3 +116,57 @@ def host_layer(oracle, layer=0, width=WIDTH, ff=FF, experts=EXPERTS, base_seed=B
         "Wsg": oracle.synth_normal(width, seed, STREAM_SHARED_GATE, GATE_SIGMA),
         "gamma": oracle.synth_uniform_pm(width, seed, STREAM_GAMMA, GAMMA_AMP),
     }
+
+
+class DeviceStack:
+    """The config-5 stack on the device: ``layers`` MoE layers, each step
+    h_{l+1} = h_l + MoE_l(RMSNorm(h_l; gamma_l)) for ``tokens`` tokens
+    (strata_norm mode 0, eps 1e-6; the layer; strata_elementwise mode 5).
+    ``trace`` keeps every layer's input and routing for checking."""
+
+    def __init__(self, backend, layers=48, tokens=1, width=WIDTH, ff=FF, experts=EXPERTS, topk=TOPK,
+                 base_seed=BASE_SEED, trace=False):
+        """``layers``: a count, or a list of existing DeviceLayer objects
+        (layer l of the list is layer l of the stack; not freed here)."""
+        self.b, self.T = backend, tokens
+        self.width, self.ff, self.experts, self.topk = width, ff, experts, topk
+        self.own_layers = not isinstance(layers, list)
+        self.layers = ([DeviceLayer(backend, l, width, ff, experts, base_seed) for l in range(layers)]
+                       if self.own_layers else layers)
+        self.L = layers = len(self.layers)
+        n = tokens * width
+        self.H = [backend.alloc(n, zero=False) for _ in range(layers + 1 if trace else 2)]
+        self.Xn, self.Y = backend.alloc(n, zero=False), backend.alloc(n, zero=False)
+        self.ids = [backend.alloc(tokens * topk, "i32") for _ in range(layers if trace else 1)]
+        self.w = [backend.alloc(tokens * topk) for _ in range(layers if trace else 1)]
+        self.ws = backend.alloc_bytes(backend.moe_workspace_bytes(tokens, width, ff, experts, topk))
+        self.trace = trace
+
+    def input(self, seed):
+        """Seeded N(0, 1) hidden states for the step's tokens, into H[0]."""
+        self.b.synth_normal(self.H[0], self.T * self.width, seed, STREAM_INPUT, 1.0)
+        return self.H[0]
+
+    def step(self):
+        """Runs every layer once; the result is in self.output()."""
+        b, W, T = self.b, self.width, self.T
+        for l, lay in enumerate(self.layers):
+            h_in = self.H[l if self.trace else l % 2]
+            h_out = self.H[l + 1 if self.trace else (l + 1) % 2]
+            ids, w = self.ids[l if self.trace else 0], self.w[l if self.trace else 0]
+            b.run("strata_norm", {"X": h_in, "W": lay.gamma, "Y": self.Xn, "cols": W, "rows": T, "weightRows": 1,
+                                  "mode": 0, "epsilon": 1e-6, "scale": 1.0}, [T, 1, 1])
+            b.moe_layer(self.Xn, T, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, self.ff, self.experts,
+                        self.topk, self.Y, ids, w, self.ws)
+            b.run("strata_elementwise", {"A": h_in, "B": self.Y, "Y": h_out, "n": T * W, "mode": 5, "scale": 1.0},
+                  [(T * W + 63) // 64, 1, 1])
+
+    def output(self):
+        return self.H[self.L if self.trace else self.L % 2]
+
+    def free(self):
+        if self.own_layers:
+            for lay in self.layers:
+                lay.free()
+        for buf in self.H + self.ids + self.w + [self.Xn, self.Y, self.ws]:
+            self.b.free(buf)

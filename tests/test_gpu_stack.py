@@ -1,0 +1,79 @@
+"""The 48-layer stack of the MoE path (h <- h + MoE_l(RMSNorm(h; gamma_l)))
+on the GPU, teacher-forced against the CPU oracle: every layer's routing is
+recomputed by the oracle from the GPU's own input to that layer, so routed
+IDs, their order and the routing weights must match bit for bit at every
+layer, and every layer's output within |a - e| <= 1e-4 + 1e-3 |e| (the f32
+trajectory itself is not bit-exact: the fused expert products only meet the
+tolerance)."""
+import numpy as np
+import pytest
+
+from conftest import tol_ok
+from stratacuda_amd import workload as wl
+
+pytestmark = pytest.mark.gpu
+
+LAYERS = 48
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def stack_layers(backend):
+    layers = [wl.DeviceLayer(backend, l) for l in range(LAYERS)]
+    yield layers
+    for lay in layers:
+        lay.free()
+
+
+def check_layer(backend, oracle, st, l, rows):
+    W, K = wl.WIDTH, wl.TOPK
+    h_in = backend.read(st.H[l]).reshape(st.T, W)
+    h_out = backend.read(st.H[l + 1]).reshape(st.T, W)
+    ids = backend.read(st.ids[l]).reshape(st.T, K)
+    w = backend.read(st.w[l]).reshape(st.T, K)
+    sub = ids[rows].reshape(-1)
+    host = wl.host_layer(oracle, l, expert_ids=sub)
+    out, eids, ew = oracle.moe_block(h_in[rows].reshape(-1), len(rows), host["gamma"], host["Wr"], host["arena"],
+                                     host["stride"], host["shared"], host["Wsg"], W, wl.FF, wl.EXPERTS, K)
+    assert np.array_equal(eids, sub), "layer %d routing differs" % l
+    assert same_bits(ew, w[rows].reshape(-1)), "layer %d routing weights differ" % l
+    got = h_out[rows].reshape(-1)
+    assert tol_ok(got, out), "layer %d output: max abs err %g" % (l, np.abs(got - out).max())
+
+
+def test_stack_decode_batch1_every_layer(backend, oracle, stack_layers):
+    st = wl.DeviceStack(backend, layers=stack_layers, tokens=1, trace=True)
+    try:
+        for step in range(2):
+            st.input(wl.BASE_SEED + 1000 + step)
+            st.step()
+            assert np.all(np.isfinite(backend.read(st.output())))
+            for l in range(LAYERS):
+                check_layer(backend, oracle, st, l, [0])
+    finally:
+        st.free()
+
+
+def test_stack_batch32(backend, oracle, stack_layers):
+    st = wl.DeviceStack(backend, layers=stack_layers, tokens=32, trace=True)
+    try:
+        st.input(wl.BASE_SEED + 2000)
+        st.step()
+        assert np.all(np.isfinite(backend.read(st.output())))
+        # routing of all 32 tokens at every layer, bit-exact, from the GPU's layer inputs
+        for l in range(LAYERS):
+            h_in = backend.read(st.H[l])
+            lay = stack_layers[l]
+            xn = oracle.norm(h_in, backend.read(lay.gamma), wl.WIDTH, 32, 1, 0, 1e-6, 1.0)
+            logits = oracle.project(xn, backend.read(lay.Wr), wl.WIDTH, wl.EXPERTS, 32)
+            rids, rw = oracle.router(logits, wl.EXPERTS, wl.TOPK, 32)
+            assert np.array_equal(backend.read(st.ids[l]), rids), "layer %d routing differs" % l
+            assert same_bits(backend.read(st.w[l]), rw), "layer %d routing weights differ" % l
+        # outputs of a few tokens at the first, middle and last layers
+        for l in (0, LAYERS // 2, LAYERS - 1):
+            check_layer(backend, oracle, st, l, [0, 13, 31])
+    finally:
+        st.free()
