@@ -95,14 +95,22 @@ def cpu_baseline(oracle, wl, seconds):
 
 PROFILE_CMDS = {
     "trace": "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/trace -o decode -- "
-             "python3 -u bench.py --no-cpu --steps 960",
+             "python3 -u bench.py --no-cpu --eager --steps 960",
     "fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o decode -- "
-             "python3 -u bench.py --no-cpu --no-prefill --layers 8 --steps 16 --warmup 8",
+             "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --layers 8 --steps 16 --warmup 8",
     "write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o decode -- "
-             "python3 -u bench.py --no-cpu --no-prefill --layers 8 --steps 16 --warmup 8",
+             "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --layers 8 --steps 16 --warmup 8",
     "cal_fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_cal_fetch -o cal -- python3 -u bench.py --calibrate",
     "cal_write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_cal_write -o cal -- python3 -u bench.py --calibrate",
 }
+for _case in ("512", "2048zipf"):
+    PROFILE_CMDS["mfma_" + _case] = (
+        "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_BUSY_CYCLES GRBM_GUI_ACTIVE "
+        "-f csv -d gpurun_out/pmc_mfma_%s -o prefill -- python3 -u bench.py --no-cpu --eager --no-stack --layers 2 "
+        "--steps 2 --warmup 2 --prefill-reps 4 --prefill-cases %s" % (_case, _case))
+MFMA_FLOP_PER_INST = 2 * 32 * 32 * 16   # v_mfma_f32_32x32x16_f16, the only MFMA the prefill kernels issue
+MFMA_CYCLES_PER_INST = 32               # busy cycles per such instruction on one SIMD
+SIMDS = 256 * 4
 DECODE_KERNELS = ["k_decode_route", "k_decode_gate_up", "k_decode_down"]
 
 
@@ -124,6 +132,54 @@ def _pmc_mean(path, counter, kernel):
     vals = [float(r["Counter_Value"]) for r in _csv_rows(path)
             if r["Counter_Name"] == counter and _kernel_key(r["Kernel_Name"]) == kernel]
     return sum(vals) / len(vals) if vals else None, len(vals)
+
+
+def _gemm_label(name):
+    """Readable name of a prefill kernel from its (possibly mangled) symbol."""
+    import re
+    m = re.search(r"k_moe_gemm_streamILb(\d)ELi(\d)ELi(\d)ELi(\d+)E", name)
+    if m:
+        return "k_moe_gemm_stream<%s, %d x %d tile, K/64 = %s>" % (
+            "gate_up" if m.group(1) == "1" else "down", 32 * int(m.group(2)), 128 * int(m.group(3)), m.group(4))
+    return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+
+def summarize_mfma(path, case, dest):
+    """MFMA use of the prefill kernels from one --pmc run: per kernel the
+    dispatches, mean duration (dispatch timestamps), MFMA instructions, the
+    FLOP/s they issue and SQ_VALU_MFMA_BUSY_CYCLES over all SIMDs at 2.4 GHz."""
+    import collections
+    per = collections.defaultdict(dict)
+    for r in _csv_rows(path):
+        d = per[r["Dispatch_Id"]]
+        d["name"] = r["Kernel_Name"]
+        d["ns"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+    agg = collections.OrderedDict()
+    for d in per.values():
+        if "gemm" not in d["name"] and "k_combine" not in d["name"] and "dispatch" not in d["name"] \
+                and "split_hilo" not in d["name"]:
+            continue
+        agg.setdefault(_gemm_label(d["name"]), []).append(d)
+    lines = ["# MFMA use of the prefill kernels, T=%s" % case.replace("zipf", " (Zipf-biased router)"), "",
+             "Command (from the repository root):", "", "    " + PROFILE_CMDS["mfma_" + case], "",
+             "Issued rate = SQ_INSTS_MFMA x %d FLOP / duration (each algorithmic product runs twice, once for the "
+             "high and once for the low fp16 half of the activations, so the algorithmic rate is half of it). "
+             "Busy = SQ_VALU_MFMA_BUSY_CYCLES / (%d SIMDs x duration x 2.4 GHz). Peak: 2.5 PFLOP/s dense fp16."
+             % (MFMA_FLOP_PER_INST, SIMDS), "",
+             "| kernel | dispatches | avg us | MFMA insts | issued TFLOP/s | issued / peak | MFMA busy | VALU insts |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, ds in agg.items():
+        n = len(ds)
+        us = sum(d["ns"] for d in ds) / n / 1e3
+        mf = sum(d.get("SQ_INSTS_MFMA", 0) for d in ds) / n
+        busy = sum(d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) for d in ds) / n
+        va = sum(d.get("SQ_INSTS_VALU", 0) for d in ds) / n
+        rate = mf * MFMA_FLOP_PER_INST / (us * 1e-6) / 1e12 if us else 0.0
+        lines.append("| %s | %d | %.1f | %.0f | %.1f | %.3f | %.3f | %.0f |" % (
+            name, n, us, mf, rate, rate * 1e12 / PEAK_MFMA_F16, busy / (SIMDS * us * 1e-6 * 2.4e9) if us else 0.0,
+            va))
+    open(dest, "w").write("\n".join(lines) + "\n")
 
 
 def summarize(out_dir):
@@ -175,6 +231,10 @@ def summarize(out_dir):
         md.append("| %s | %d | %.1f | %.1f | %d | %d | %.2f |" % (k, n, fk, wk, t, algo_by_kernel[k],
                                                                  t / algo_by_kernel[k]))
     json.dump(traffic, open(os.path.join(prof, "traffic.json"), "w"), indent=1)
+    for case in ("512", "2048zipf"):
+        found = glob.glob(os.path.join(out_dir, "pmc_mfma_" + case, "*counter_collection.csv"))
+        if found:
+            summarize_mfma(found[0], case, os.path.join(prof, "mfma_prefill_T%s.md" % case))
     open(os.path.join(prof, "traffic_decode_T1.md"), "w").write("\n".join(md) + "\n")
     print(json.dumps({"summaries": sorted(os.listdir(prof)), "traffic": traffic}))
 
@@ -189,8 +249,12 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack runs")
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="issue every step directly instead of replaying HIP graphs (for profilers)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--prefill-cases", default="512,2048zipf",
+                    help="comma-separated prefill cases: token count, 'zipf' for the Zipf-biased router")
     ap.add_argument("--summarize", metavar="DIR",
                     help="write the profiles/ summaries from rocprofv3 CSVs under DIR (no GPU needed)")
     ap.add_argument("--calibrate", action="store_true",
@@ -250,26 +314,40 @@ def main():
         assert np.all(np.isfinite(be.read(s["y"])))
 
     # ---- timed region: exactly K steps from graph replays
-    be.graph_begin()
-    for i in range(L):
-        step(i)
-    g_full = be.graph_end()
-    rem = args.steps % L
-    g_rem = None
-    if rem:
+    def capture(fn):
+        """A graph of what fn issues, or fn itself with --eager."""
+        if args.eager:
+            return fn
         be.graph_begin()
-        for i in range(rem):
+        fn()
+        return be.graph_end()
+
+    def replay(g):
+        if args.eager:
+            g()
+        else:
+            be.graph_launch(g)
+
+    def release(g):
+        if not args.eager:
+            be.graph_free(g)
+
+    def all_layers(count=L):
+        for i in range(count):
             step(i)
-        g_rem = be.graph_end()
-    be.graph_launch(g_full)  # warm the graph itself
+
+    g_full = capture(all_layers)
+    rem = args.steps % L
+    g_rem = capture(lambda: all_layers(rem)) if rem else None
+    replay(g_full)  # warm the graph itself
     be.sync()
     be.sync()
     t0 = time.perf_counter()
     be.event_record(0)
     for _ in range(args.steps // L):
-        be.graph_launch(g_full)
+        replay(g_full)
     if g_rem is not None:
-        be.graph_launch(g_rem)
+        replay(g_rem)
     be.event_record(1)
     be.sync()
     t1 = time.perf_counter()
@@ -283,23 +361,22 @@ def main():
     reps = max(1, min(50, 2400 // L))
     for stage, name in enumerate(["decode_route", "decode_gate_up", "decode_down_combine"]):
         be.stage_select(1 << stage)
-        be.graph_begin()
-        for i in range(L):
-            step(i)
-        gid = be.graph_end()
-        be.stage_select()
-        be.graph_launch(gid)
+        gid = capture(all_layers)
+        if not args.eager:
+            be.stage_select()
+        replay(gid)
         be.sync()
         be.event_record(2)
         for _ in range(reps):
-            be.graph_launch(gid)
+            replay(gid)
         be.event_record(3)
         be.sync()
+        be.stage_select()
         us = be.event_elapsed_ms(2, 3) * 1e3 / (reps * L)
         gbs = kernel_bytes[name] / (us * 1e-6) / 1e9
         kernels[name] = {"avg_us": round(us, 3), "bytes_per_launch": kernel_bytes[name], "GB/s": round(gbs, 1),
                          "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4)}
-        be.graph_free(gid)
+        release(gid)
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
     hip_kernel = {"decode_route": "k_decode_route", "decode_gate_up": "k_decode_gate_up",
                   "decode_down_combine": "k_decode_down"}[dom]
@@ -317,7 +394,8 @@ def main():
     prefill = None
     if not args.no_prefill:
         prefill = {}
-        for T, zipf in ((512, False), (2048, True)):
+        cases = [(int(c.replace("zipf", "")), "zipf" in c) for c in args.prefill_cases.split(",") if c]
+        for T, zipf in cases:
             Xs = []
             for j in range(2):
                 X = be.alloc(T * W, zero=False)
@@ -377,17 +455,15 @@ def main():
             S = args.stack_steps
             inputs = be.alloc(S * T * W, zero=False)
             be.synth_normal(inputs, S * T * W, wl.BASE_SEED + 31 * T, wl.STREAM_INPUT, 1.0)
-            be.graph_begin()
-            st.step()
-            gid = be.graph_end()
+            gid = capture(st.step)
             for s in range(2):
                 be.copy(inputs, st.H[0], T * W, s * T * W, 0)
-                be.graph_launch(gid)
+                replay(gid)
             be.sync()
             be.event_record(6)
             for s in range(S):
                 be.copy(inputs, st.H[0], T * W, s * T * W, 0)
-                be.graph_launch(gid)
+                replay(gid)
             be.event_record(7)
             be.sync()
             ms = be.event_elapsed_ms(6, 7) / S
@@ -400,7 +476,7 @@ def main():
                         "frac": round(step_bytes / (ms * 1e-3) / PEAK_HBM, 4)},
                 "execution": "one HIP graph per step: per layer RMSNorm, MoE layer, residual add",
             }
-            be.graph_free(gid)
+            release(gid)
             be.free(inputs)
             st.free()
 

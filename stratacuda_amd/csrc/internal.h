@@ -12,6 +12,10 @@
 struct sm_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    // Second stream (default priority) for independent work inside one call,
+    // forked from and joined back to `stream` with the two events.
+    hipStream_t aux = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     std::map<uint64_t, uint64_t> buffers;  // handle (device address) -> bytes
     std::string error;
     hipEvent_t events[64] = {};
@@ -45,6 +49,11 @@ int hip_fail(sm_ctx *ctx, hipError_t err, const char *what);
 // Checks that `handle` is a live allocation holding at least `bytes` bytes.
 int need(sm_ctx *ctx, uint64_t handle, uint64_t bytes, const char *what);
 int launched(sm_ctx *ctx);  // checks hipGetLastError after a launch
+// fork_aux: work queued on ctx->aux after this runs after everything queued on
+// ctx->stream so far. join_aux: work queued on ctx->stream after this runs
+// after everything queued on ctx->aux so far. Both are graph-capturable.
+int fork_aux(sm_ctx *ctx);
+int join_aux(sm_ctx *ctx);
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -97,6 +97,47 @@ __device__ __forceinline__ half8 b_operand(uint4 c, int s, int kh, half2v scale)
     return b;
 }
 
+// B operand of the streaming kernel, three VALU operations per pair. The lane
+// works on w' = word >> 8 kh, whose pair q (q = 0..3) sits at bits 2q and
+// 2q + 16, i.e. codes (p, p + 8) with p = 4 kh + q. OR-ing the masked bits
+// under the fp16 exponent 10 - 2q makes each code the units digit of
+// 2^(10-2q) + c; subtracting 2^(10-2q) + 1 leaves c - 1 exactly, and the
+// product with the fp16 scale is exact. No per-pair shift is needed.
+struct PairMagic {
+    uint32_t mask[4];  // 0x00030003 << 2q, held in VGPRs (v_and_or_b32 takes one SGPR)
+};
+__device__ __forceinline__ PairMagic pair_magic() {
+    PairMagic m;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        m.mask[q] = 0x00030003u << (2 * q);
+        asm volatile("" : "+v"(m.mask[q]));
+    }
+    return m;
+}
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "s"(bits));
+    return r;
+}
+template <int Q>
+__device__ __forceinline__ half2v pair_q(uint32_t wq, const PairMagic &m, half2v scale) {
+    constexpr uint32_t e = 25 - 2 * Q;                  // biased exponent of 2^(10-2q)
+    constexpr uint32_t magic = (e << 10) | (e << 26);
+    constexpr float sub = (float)((1 << (10 - 2 * Q)) + 1);
+    const half2v h = __builtin_bit_cast(half2v, and_or_b32(wq, m.mask[Q], magic));
+    const half2v k = {(_Float16)sub, (_Float16)sub};
+    return (h - k) * scale;
+}
+__device__ __forceinline__ half8 b_operand_stream(uint4 c, int s, uint32_t shift, const PairMagic &m,
+                                                  half2v scale) {
+    const uint32_t w = (s == 0 ? c.x : s == 1 ? c.y : s == 2 ? c.z : c.w) >> shift;
+    const half2v p0 = pair_q<0>(w, m, scale), p1 = pair_q<1>(w, m, scale);
+    const half2v p2 = pair_q<2>(w, m, scale), p3 = pair_q<3>(w, m, scale);
+    const half8 b = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+    return b;
+}
+
 // Segment lookup: largest e with tile_base[e] <= tau (segments 0..nseg-1).
 __device__ __forceinline__ int find_segment(const int *tile_base, int nseg, int tau) {
     int lo = 0, hi = nseg - 1;
@@ -266,9 +307,9 @@ __global__ void __launch_bounds__(64 * WM * WN) k_moe_gemm(const _Float16 *__res
 
 // ---------------------------------------------------------------------------
 // Streaming grouped GEMM: the same tiles and arithmetic as k_moe_gemm, fed by
-// a ring of three stages (one 64-wide scale group each) filled with direct
+// a ring of stages (one 64-wide scale group each) filled with direct
 // global->LDS loads (global_load_lds_dwordx4: lane l of a wave writes 16 bytes
-// at the instruction's LDS base + 16 l), so two groups of A and B are in
+// at the instruction's LDS base + 16 l), so the next groups of A and B are in
 // flight while the current one is multiplied, without occupying registers.
 // The group count K / 64 is a template parameter, so the ring is unrolled
 // into straight-line code and the compiler's own waits match the ring's.
@@ -277,8 +318,8 @@ __global__ void __launch_bounds__(64 * WM * WN) k_moe_gemm(const _Float16 *__res
 // below. Every thread issues the same number of loads per stage (rows past a
 // segment's end load a valid row; those results are never stored), so one
 // compile-time vmcnt covers all waves. 4 waves side by side in N: block tile
-// (32 MI) x (128 NI), wave tile (32 MI) x (32 NI). Scale planes of the block's
-// weight rows (K <= 2048) are loaded once into LDS.
+// (32 MI) x (128 NI), wave tile (32 MI) x (32 NI). Each lane keeps the scales
+// of its weight rows (every group, K <= 2048) in registers.
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ void dma16(const void *src, void *lds_base) {
@@ -302,8 +343,8 @@ constexpr int STREAM_MAX_G = 32;  // K <= 2048 for the streaming kernel
 // Ring stages. Each stage is a separate object at namespace scope: the
 // compiler's wait insertion then tells loads into one stage from reads of
 // another (stages declared inside the kernel made it wait for every load
-// before any read). Big tiles (64 x 256) use three stages, small tiles
-// (32 x 256) five; the scale planes of the block's weight rows sit beside.
+// before any read). Big tiles (64 x 256) use three stages (60 KiB, two
+// blocks per CU), small tiles (32 x 256) four (48 KiB, three blocks per CU).
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 template <int BM>
 struct RingStage {
@@ -311,8 +352,7 @@ struct RingStage {
     v4u b[256];      // [weight row] 16 B of codes (the tail is filler for 128-wide tiles)
 };
 __shared__ __attribute__((aligned(16))) RingStage<64> g_big0, g_big1, g_big2;
-__shared__ __attribute__((aligned(16))) RingStage<32> g_small0, g_small1, g_small2, g_small3, g_small4;
-__shared__ __attribute__((aligned(16))) uint16_t g_stream_scale[256 * STREAM_MAX_G];
+__shared__ __attribute__((aligned(16))) RingStage<32> g_small0, g_small1, g_small2, g_small3;
 
 template <int BM>
 struct Ring;
@@ -326,10 +366,10 @@ struct Ring<64> {
 };
 template <>
 struct Ring<32> {
-    static constexpr int NS = 5;
+    static constexpr int NS = 4;
     template <int S>
     static __device__ __forceinline__ RingStage<32> &stage() {
-        return S == 0 ? g_small0 : S == 1 ? g_small1 : S == 2 ? g_small2 : S == 3 ? g_small3 : g_small4;
+        return S == 0 ? g_small0 : S == 1 ? g_small1 : S == 2 ? g_small2 : g_small3;
     }
 };
 // Calls f(stage S) for the S equal to `slot` (slot is a constant once the
@@ -364,8 +404,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     constexpr int BM = P::BM, BN = P::BN, ACH = P::ACH, BCH = P::BCH;
     using Stage = RingStage<BM>;
     constexpr int NS = Ring<BM>::NS;
-    uint16_t *s_scale = g_stream_scale;
-    static_assert(KG >= 1 && KG <= STREAM_MAX_G, "K / 64 groups");
+    static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 8 == 0, "K / 64 groups");
     static_assert(BM <= 64 && BN <= 256, "stage size");
     const int nseg = experts + 1;
     const int tau = blockIdx.y;
@@ -403,28 +442,29 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
 #pragma unroll
         for (int i = 0; i < BCH; i++) dma16(bsrc[i] + (uint64_t)g * 16, &sg.b[256 * i + 64 * wave]);
     };
-    // Scales of the block's BN rows, all groups, stored [group][row] in LDS so
-    // that the lanes of a wave read consecutive halves. The plane is
-    // [row][G] in memory: read as 16-byte chunks (8 consecutive scales of
-    // the flattened range, possibly spanning rows), written out by element.
-    {
-        const uint8_t *base = blob + scales_off + (uint64_t)n0 * G * 2;
-        const int chunks = BN * G * 2 / 16;
-        for (int c = tid; c < chunks; c += 256) {
-            const uint4 v = *(const uint4 *)(base + (uint64_t)c * 16);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const int j = lane & 31, kh = lane >> 5;
+    // Scales of the lane's weight rows, every group, in registers: the plane
+    // is [row][G] fp16, so a row is 2G contiguous bytes and the 32 lanes of a
+    // half-wave read 32 consecutive rows. Issued before the ring, so the
+    // ring's first wait also covers them.
+    uint32_t sreg[NI][G / 2];
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int flat = c * 8 + q, row = flat / G, grp = flat - row * G;
-                s_scale[grp * BN + row] = (uint16_t)(w[q >> 1] >> (16 * (q & 1)));
-            }
+    for (int ni = 0; ni < NI; ni++) {
+        const uint4 *sp = (const uint4 *)(blob + scales_off + (uint64_t)(n0 + wave * 32 * NI + ni * 32 + j) * G * 2);
+#pragma unroll
+        for (int c = 0; c < G / 8; c++) {
+            const uint4 v = sp[c];
+            sreg[ni][4 * c + 0] = v.x;
+            sreg[ni][4 * c + 1] = v.y;
+            sreg[ni][4 * c + 2] = v.z;
+            sreg[ni][4 * c + 3] = v.w;
         }
     }
-    __syncthreads();
 #pragma clang loop unroll(full)
     for (int q = 0; q < NS - 1; q++) with_stage<BM>(q, [&](Stage &sg) { issue(sg, min(q, G - 1)); });
 
-    const int j = lane & 31, kh = lane >> 5;
+    const PairMagic magic = pair_magic();
+    const uint32_t shift = 8 * kh;
     float16v acc[MI][NI];
 #pragma unroll
     for (int mi = 0; mi < MI; mi++)
@@ -441,14 +481,15 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
             const int nl = wave * 32 * NI + ni * 32 + j;
             const v4u cv = sg.b[nl];
             codes[ni] = make_uint4(cv.x, cv.y, cv.z, cv.w);
-            const _Float16 s16 = __builtin_bit_cast(_Float16, s_scale[g * BN + nl]);
-            scale[ni] = (half2v){s16, s16};
+            const uint16_t s16 = (uint16_t)(sreg[ni][g >> 1] >> (16 * (g & 1)));
+            const _Float16 sh = __builtin_bit_cast(_Float16, s16);
+            scale[ni] = (half2v){sh, sh};
         }
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             half8 b[NI];
 #pragma unroll
-            for (int ni = 0; ni < NI; ni++) b[ni] = b_operand(codes[ni], s, kh, scale[ni]);
+            for (int ni = 0; ni < NI; ni++) b[ni] = b_operand_stream(codes[ni], s, shift, magic, scale[ni]);
 #pragma unroll
             for (int mi = 0; mi < MI; mi++) {
                 const int r = mi * 32 + j, slot = (2 * s + kh) ^ ((r >> 1) & 7);
@@ -617,14 +658,23 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         if (N % 256 == 0 && (K == 2048 || K == 512)) {
             auto kb = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 2, 2, 32> : k_moe_gemm_stream<true, 2, 2, 8>)
                               : (K == 2048 ? k_moe_gemm_stream<false, 2, 2, 32> : k_moe_gemm_stream<false, 2, 2, 8>);
-            kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->stream>>>(a, r, offsets, tiles_big, ar, blob_stride,
-                                                                             sh, experts, codes, scales, K, N, out, ld);
-            if (int rc = launched(ctx)) return rc;
+            // The two tilings cover disjoint rows: the big-tile grid (few,
+            // long blocks at small T) runs on the second stream beside the
+            // small-tile grid.
+            if (int rc = fork_aux(ctx)) return rc;
+            kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(a, r, offsets, tiles_big, ar, blob_stride,
+                                                                          sh, experts, codes, scales, K, N, out, ld);
+            const int rc_big = launched(ctx);
             auto ks = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 1, 2, 32> : k_moe_gemm_stream<true, 1, 2, 8>)
                               : (K == 2048 ? k_moe_gemm_stream<false, 1, 2, 32> : k_moe_gemm_stream<false, 1, 2, 8>);
-            ks<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
-                a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
-            return launched(ctx);
+            int rc_small = SM_OK;
+            if (rc_big == SM_OK) {
+                ks<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
+                    a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+                rc_small = launched(ctx);
+            }
+            const int rc_join = join_aux(ctx);
+            return rc_big ? rc_big : rc_small ? rc_small : rc_join;
         }
         if (N % 512 == 0) {
             auto kb = gate_up ? k_moe_gemm<true, 2, 2, 1, 8> : k_moe_gemm<false, 2, 2, 1, 8>;

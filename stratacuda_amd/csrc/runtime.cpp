@@ -37,6 +37,18 @@ int launched(sm_ctx *ctx) {
     return SM_OK;
 }
 
+int fork_aux(sm_ctx *ctx) {
+    hipError_t err = hipEventRecord(ctx->fork, ctx->stream);
+    if (err == hipSuccess) err = hipStreamWaitEvent(ctx->aux, ctx->fork, 0);
+    return err == hipSuccess ? SM_OK : hip_fail(ctx, err, "stream fork");
+}
+
+int join_aux(sm_ctx *ctx) {
+    hipError_t err = hipEventRecord(ctx->join, ctx->aux);
+    if (err == hipSuccess) err = hipStreamWaitEvent(ctx->stream, ctx->join, 0);
+    return err == hipSuccess ? SM_OK : hip_fail(ctx, err, "stream join");
+}
+
 // Folds recorded stage events into the per-stage totals (synchronises).
 static int stage_fold(sm_ctx *ctx) {
     if (ctx->marks.empty()) return SM_OK;
@@ -94,6 +106,12 @@ int sm_init(int device, sm_ctx **out) {
         delete ctx;
         return SM_E_HIP;
     }
+    if (hipStreamCreateWithFlags(&ctx->aux, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess) {
+        sm_shutdown(ctx);
+        return SM_E_HIP;
+    }
     for (auto &e : ctx->events) {
         if (hipEventCreate(&e) != hipSuccess) {
             sm_shutdown(ctx);
@@ -113,6 +131,7 @@ void sm_shutdown(sm_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->aux) (void)hipStreamSynchronize(ctx->aux);
     for (auto &kv : ctx->buffers) (void)hipFree((void *)kv.first);
     ctx->buffers.clear();
     if (ctx->counters) (void)hipFree(ctx->counters);
@@ -121,6 +140,9 @@ void sm_shutdown(sm_ctx *ctx) {
         if (g) (void)hipGraphExecDestroy(g);
     for (auto &e : ctx->events)
         if (e) (void)hipEventDestroy(e);
+    if (ctx->fork) (void)hipEventDestroy(ctx->fork);
+    if (ctx->join) (void)hipEventDestroy(ctx->join);
+    if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
