@@ -100,9 +100,12 @@ int sm_moe_route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, ui
 /* Expert-contiguous dispatch of routed IDs: experts ascending, tokens
  * ascending within an expert (the within-expert order of src/prefill.js:56-61).
  * offsets [experts+1] exclusive scan of counts; rows[pos] = token;
- * parts[pos] = token*topk + k; where[token*topk + k] = pos. Fails with
- * SM_E_ROUTE if an ID is out of range or repeated within a token
- * (src/engine.js:138, src/prefill.js:57). */
+ * parts[pos] = token*topk + k; where[token*topk + k] = pos. The checks of
+ * src/engine.js:138 / src/prefill.js:57 run on the device, asynchronously:
+ * an ID out of range is left out (where = -1) and sets bit 0 of the uint32
+ * at workspace offset 0, an ID repeated within a token sets bit 1; the word
+ * is 0 when every ID is valid. workspace_bytes of sm_moe_layer_workspace()
+ * for the same shape always suffice (SM_E_ARG when too small). */
 int sm_moe_dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets,
                     uint64_t rows, uint64_t parts, uint64_t where_, uint64_t workspace,
                     uint64_t workspace_bytes);

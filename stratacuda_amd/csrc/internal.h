@@ -83,10 +83,13 @@ int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float
                  int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out);
 // M-tile bases the dispatch writes for the grouped GEMMs: segments with at
 // least `split` rows in tiles of mt_big rows (big[]), the others in tiles of
-// mt_small rows (small[]); each array has experts + 2 entries.
+// mt_small rows (small[]); each array has experts + 2 entries. When set,
+// info_small / info_big receive one record of 4 ints per tile: segment,
+// first row, end row of the segment, 0.
 struct GemmTiling {
     int *small, *big;
     int split, mt_small, mt_big;
+    int *info_small = nullptr, *info_big = nullptr;
 };
 int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int experts, int *offsets, int *rows, int *parts,
                     int *where_, char *workspace, int extra_rows, const GemmTiling *tiling);

@@ -60,15 +60,26 @@ __device__ __forceinline__ int k_position(int r) {
 }
 
 // X [rows x K] f32 -> hi/lo fp16 [rows][K/64][2][64] in the MFMA K order.
-__global__ void k_split_hilo(const float *__restrict__ X, _Float16 *__restrict__ out, int64_t groups) {
+__global__ void __launch_bounds__(256) k_split_hilo(const float *__restrict__ X, _Float16 *__restrict__ out,
+                                                    int64_t groups) {
+    // Thread (group rg, chunk c) writes positions 8c .. 8c+7 of the group's
+    // hi and lo halves: elements 16w + 4h + {0, 8, 1, 9, 2, 10, 3, 11} with
+    // w = c / 2, h = c % 2, i.e. two float4 reads and two 16-byte writes.
     const int64_t at = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t rg = at >> 6;
+    const int64_t rg = at >> 3;
     if (rg >= groups) return;
-    const int q = (int)(at & 63), w = q >> 4, t = q & 15;
-    const float x = X[rg * 64 + 16 * w + (t >> 1) + 8 * (t & 1)];
-    const _Float16 hi = (_Float16)x;
-    out[rg * 128 + q] = hi;
-    out[rg * 128 + 64 + q] = (_Float16)(x - (float)hi);
+    const int c = (int)(at & 7), src = 16 * (c >> 1) + 4 * (c & 1);
+    const float4 a = *(const float4 *)(X + rg * 64 + src), b = *(const float4 *)(X + rg * 64 + src + 8);
+    const float x[8] = {a.x, b.x, a.y, b.y, a.z, b.z, a.w, b.w};
+    half8 hi, lo;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const _Float16 h = (_Float16)x[u];
+        hi[u] = h;
+        lo[u] = (_Float16)(x[u] - (float)h);
+    }
+    *(half8 *)(out + rg * 128 + 8 * c) = hi;
+    *(half8 *)(out + rg * 128 + 64 + 8 * c) = lo;
 }
 
 // SiLU for the fused prefill epilogue, whose outputs are checked to a
@@ -129,24 +140,16 @@ __device__ __forceinline__ half2v pair_q(uint32_t wq, const PairMagic &m, half2v
     const half2v k = {(_Float16)sub, (_Float16)sub};
     return (h - k) * scale;
 }
-__device__ __forceinline__ half8 b_operand_stream(uint4 c, int s, uint32_t shift, const PairMagic &m,
-                                                  half2v scale) {
-    const uint32_t w = (s == 0 ? c.x : s == 1 ? c.y : s == 2 ? c.z : c.w) >> shift;
+// The four pairs of an already shifted word w'.
+__device__ __forceinline__ half8 b_operand_word(uint32_t w, const PairMagic &m, half2v scale) {
     const half2v p0 = pair_q<0>(w, m, scale), p1 = pair_q<1>(w, m, scale);
     const half2v p2 = pair_q<2>(w, m, scale), p3 = pair_q<3>(w, m, scale);
     const half8 b = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     return b;
 }
-
-// Segment lookup: largest e with tile_base[e] <= tau (segments 0..nseg-1).
-__device__ __forceinline__ int find_segment(const int *tile_base, int nseg, int tau) {
-    int lo = 0, hi = nseg - 1;
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (tile_base[mid] <= tau) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
+__device__ __forceinline__ half8 b_operand_stream(uint4 c, int s, uint32_t shift, const PairMagic &m,
+                                                  half2v scale) {
+    return b_operand_word((s == 0 ? c.x : s == 1 ? c.y : s == 2 ? c.z : c.w) >> shift, m, scale);
 }
 
 // GATE_UP: A = X (hi/lo) rows gathered through rows[], K = width, N = 2*ff;
@@ -156,7 +159,7 @@ __device__ __forceinline__ int find_segment(const int *tile_base, int nseg, int 
 //          [positions x width].
 template <bool GATE_UP, int MI, int NI, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN) k_moe_gemm(const _Float16 *__restrict__ A, const int *__restrict__ rows,
-                                                  const int *__restrict__ offsets, const int *__restrict__ tiles,
+                                                  const int4 *__restrict__ info, const int *__restrict__ tiles,
                                                   const uint8_t *__restrict__ arena, uint64_t stride,
                                                   const uint8_t *__restrict__ shared_blob, int experts,
                                                   uint64_t codes_off, uint64_t scales_off, int K, int N,
@@ -164,11 +167,11 @@ __global__ void __launch_bounds__(64 * WM * WN) k_moe_gemm(const _Float16 *__res
     constexpr int THREADS = 64 * WM * WN, BM = 32 * MI * WM, BN = 32 * NI * WN;
     constexpr int ACH = (BM * 16 + THREADS - 1) / THREADS;  // 16-byte A chunks per thread and group
     __shared__ __attribute__((aligned(16))) _Float16 lds[2][2 * BM * APITCH];  // [buf][hi/lo][row][APITCH]
-    const int nseg = experts + 1;
+    // Tile record (segment, first row, end of the segment) from the dispatch.
     const int tau = blockIdx.y;
-    if (tau >= tiles[nseg]) return;
-    const int e = find_segment(tiles, nseg, tau);
-    const int m0 = offsets[e] + (tau - tiles[e]) * BM, mend = offsets[e + 1];
+    if (tau >= tiles[experts + 1]) return;
+    const int4 ti = info[tau];
+    const int e = ti.x, m0 = ti.y, mend = ti.z;
     const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -344,7 +347,7 @@ constexpr int STREAM_MAX_G = 32;  // K <= 2048 for the streaming kernel
 // compiler's wait insertion then tells loads into one stage from reads of
 // another (stages declared inside the kernel made it wait for every load
 // before any read). Big tiles (64 x 256) use three stages (60 KiB, two
-// blocks per CU), small tiles (32 x 256) four (48 KiB, three blocks per CU).
+// blocks per CU).
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 template <int BM>
 struct RingStage {
@@ -352,7 +355,6 @@ struct RingStage {
     v4u b[256];      // [weight row] 16 B of codes (the tail is filler for 128-wide tiles)
 };
 __shared__ __attribute__((aligned(16))) RingStage<64> g_big0, g_big1, g_big2;
-__shared__ __attribute__((aligned(16))) RingStage<32> g_small0, g_small1, g_small2, g_small3;
 
 template <int BM>
 struct Ring;
@@ -364,12 +366,15 @@ struct Ring<64> {
         return S == 0 ? g_big0 : S == 1 ? g_big1 : g_big2;
     }
 };
+// 16-row tiles (k_moe_gemm_stream16): 8 KiB stages, six of them (48 KiB,
+// three blocks per CU).
+__shared__ __attribute__((aligned(16))) RingStage<16> g_tiny0, g_tiny1, g_tiny2, g_tiny3, g_tiny4, g_tiny5;
 template <>
-struct Ring<32> {
-    static constexpr int NS = 4;
+struct Ring<16> {
+    static constexpr int NS = 6;
     template <int S>
-    static __device__ __forceinline__ RingStage<32> &stage() {
-        return S == 0 ? g_small0 : S == 1 ? g_small1 : S == 2 ? g_small2 : g_small3;
+    static __device__ __forceinline__ RingStage<16> &stage() {
+        return S == 0 ? g_tiny0 : S == 1 ? g_tiny1 : S == 2 ? g_tiny2 : S == 3 ? g_tiny3 : S == 4 ? g_tiny4 : g_tiny5;
     }
 };
 // Calls f(stage S) for the S equal to `slot` (slot is a constant once the
@@ -381,7 +386,8 @@ __device__ __forceinline__ void with_stage(int slot, F &&f) {
     case 1: f(Ring<BM>::template stage<1 % Ring<BM>::NS>()); break;
     case 2: f(Ring<BM>::template stage<2 % Ring<BM>::NS>()); break;
     case 3: f(Ring<BM>::template stage<3 % Ring<BM>::NS>()); break;
-    default: f(Ring<BM>::template stage<4 % Ring<BM>::NS>()); break;
+    case 4: f(Ring<BM>::template stage<4 % Ring<BM>::NS>()); break;
+    default: f(Ring<BM>::template stage<5 % Ring<BM>::NS>()); break;
     }
 }
 
@@ -395,7 +401,7 @@ struct StreamGemm {
 
 template <bool GATE_UP, int MI, int NI, int KG>
 __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restrict__ A, const int *__restrict__ rows,
-                                                         const int *__restrict__ offsets, const int *__restrict__ tiles,
+                                                         const int4 *__restrict__ info, const int *__restrict__ tiles,
                                                          const uint8_t *__restrict__ arena, uint64_t stride,
                                                          const uint8_t *__restrict__ shared_blob, int experts,
                                                          uint64_t codes_off, uint64_t scales_off, int K, int N,
@@ -406,11 +412,11 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     constexpr int NS = Ring<BM>::NS;
     static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 8 == 0, "K / 64 groups");
     static_assert(BM <= 64 && BN <= 256, "stage size");
-    const int nseg = experts + 1;
+    // Tile record (segment, first row, end of the segment) from the dispatch.
     const int tau = blockIdx.y;
-    if (tau >= tiles[nseg]) return;
-    const int e = find_segment(tiles, nseg, tau);
-    const int m0 = offsets[e] + (tau - tiles[e]) * BM, mend = offsets[e + 1];
+    if (tau >= tiles[experts + 1]) return;
+    const int4 ti = info[tau];
+    const int e = ti.x, m0 = ti.y, mend = ti.z;
     const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int G = KG;  // K / 64, fixed at compile time: the ring is straight-line code
@@ -545,6 +551,137 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
             }
 }
 
+// The streaming kernel for short segments: 16-row tiles on
+// v_mfma_f32_16x16x32_f16, so a segment of ~10 rows (the typical expert at a
+// few hundred tokens) pays for 16 rows of MFMA work instead of 32. Block:
+// 16 rows x 256 weight rows, 4 waves side by side in N, each 16 x 64 (four
+// 16 x 16 tiles). The 16x16x32 operands: lane l holds row (or column) l % 16
+// and K positions 8 (l / 16) .. +7 of a 32-wide step. With the K order of the
+// activations, step s of a 64-wide group and lane quarter kq = l / 16 map to
+// code word 2s + kq / 2, byte half kq % 2 (the same unpacking as the 32-row
+// kernel's lane halves) and to the 16-byte part 4s + kq of the A row.
+// Result: lane l holds rows 4 (l / 16) + i (i = 0..3) of column l % 16.
+typedef float float4v __attribute__((ext_vector_type(4)));
+template <bool GATE_UP, int KG>
+__global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__restrict__ A, const int *__restrict__ rows,
+                                                           const int4 *__restrict__ info,
+                                                           const int *__restrict__ tiles,
+                                                           const uint8_t *__restrict__ arena, uint64_t stride,
+                                                           const uint8_t *__restrict__ shared_blob, int experts,
+                                                           uint64_t codes_off, uint64_t scales_off, int K, int N,
+                                                           void *__restrict__ out, int out_ld) {
+    constexpr int BM = 16, BN = 256, NT = 4;  // NT tiles of 16 columns per wave
+    using Stage = RingStage<BM>;
+    constexpr int NS = Ring<BM>::NS;
+    constexpr int G = KG;  // K / 64
+    static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 8 == 0, "K / 64 groups");
+    (void)K;
+    (void)N;
+    // Tile record (segment, first row, end of the segment) from the dispatch.
+    const int tau = blockIdx.y;
+    if (tau >= tiles[experts + 1]) return;
+    const int4 ti = info[tau];
+    const int e = ti.x, m0 = ti.y, mend = ti.z;
+    const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * BN;
+
+    // DMA sources, one A and one B load per thread per stage. A chunk
+    // c = tid: hi/lo c / 128, row (c / 8) % 16, slot c % 8 holding part
+    // slot ^ ((row / 2) & 7).
+    const _Float16 *asrc;
+    {
+        const int hl = tid >> 7, r = (tid >> 3) & 15, part = (tid & 7) ^ ((r >> 1) & 7);
+        const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
+        const int64_t arow = GATE_UP ? rows[pos] : pos;
+        asrc = A + (arow * G * 2 + hl) * 64 + part * 8;
+    }
+    const uint8_t *bsrc = blob + codes_off + (uint64_t)(n0 + tid) * (G * 16);
+    auto issue = [&](Stage &sg, int g) {
+        dma16(asrc + (int64_t)g * 128, &sg.a[64 * wave]);
+        dma16(bsrc + (uint64_t)g * 16, &sg.b[64 * wave]);
+    };
+    const int col = lane & 15, kq = lane >> 4;
+    // Scales of the lane's four weight rows, every group, in registers.
+    uint32_t sreg[NT][G / 2];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const uint4 *sp = (const uint4 *)(blob + scales_off + (uint64_t)(n0 + wave * 64 + nt * 16 + col) * G * 2);
+#pragma unroll
+        for (int c = 0; c < G / 8; c++) {
+            const uint4 v = sp[c];
+            sreg[nt][4 * c + 0] = v.x;
+            sreg[nt][4 * c + 1] = v.y;
+            sreg[nt][4 * c + 2] = v.z;
+            sreg[nt][4 * c + 3] = v.w;
+        }
+    }
+#pragma clang loop unroll(full)
+    for (int q = 0; q < NS - 1; q++) with_stage<BM>(q, [&](Stage &sg) { issue(sg, min(q, G - 1)); });
+
+    const PairMagic magic = pair_magic();
+    const uint32_t shift = 8 * (kq & 1);
+    float4v acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) acc[nt] = (float4v){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const Stage &sg, int g) {
+        uint32_t words[NT][2];  // the lane's code word of step 0 and 1, shifted
+        half2v scale[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const v4u cv = sg.b[wave * 64 + nt * 16 + col];
+            words[nt][0] = (kq & 2 ? cv.y : cv.x) >> shift;
+            words[nt][1] = (kq & 2 ? cv.w : cv.z) >> shift;
+            const uint16_t s16 = (uint16_t)(sreg[nt][g >> 1] >> (16 * (g & 1)));
+            const _Float16 sh = __builtin_bit_cast(_Float16, s16);
+            scale[nt] = (half2v){sh, sh};
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int part = 4 * s + kq, slot = part ^ ((col >> 1) & 7);
+            const half8 ahi = __builtin_bit_cast(half8, sg.a[col * 8 + slot]);
+            const half8 alo = __builtin_bit_cast(half8, sg.a[(BM + col) * 8 + slot]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const half8 b = b_operand_word(words[nt][s], magic, scale[nt]);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, acc[nt], 0, 0, 0);
+            }
+        }
+    };
+    constexpr int PS = 2;  // loads per thread per stage
+#pragma clang loop unroll(full)
+    for (int g = 0; g < G; g++) {
+        ring_sync<PS * (NS - 2)>();
+        with_stage<BM>((g + NS - 1) % NS, [&](Stage &sg) { issue(sg, min(g + NS - 1, G - 1)); });
+        with_stage<BM>(g % NS, [&](Stage &sg) { compute(sg, g); });
+    }
+    // No load may still be writing LDS when the block ends.
+    ring_sync<0>();
+
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int pos = m0 + 4 * kq + i, n = n0 + wave * 64 + nt * 16 + col;
+            if (GATE_UP) {
+                const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[nt][i], acc[nt][i]);
+                if ((col & 1) == 0 && pos < mend) {
+                    const float h = silu_fast(acc[nt][i]) * other;
+                    const int jj = n >> 1;
+                    _Float16 *dst =
+                        (_Float16 *)out + ((int64_t)pos * (out_ld / 64) + (jj >> 6)) * 128 + k_position(jj & 63);
+                    const _Float16 hi = (_Float16)h;
+                    dst[0] = hi;
+                    dst[64] = (_Float16)(h - (float)hi);
+                }
+            } else if (pos < mend) {
+                ((float *)out)[(int64_t)pos * out_ld + n] = acc[nt][i];
+            }
+        }
+}
+
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
 // in the reference order (kernels/strata.cu:470-476). One block per token:
 // the token's slot positions, weights and sigmoid(gate) are read once, then
@@ -587,8 +724,17 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, co
 constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
+// Grid bounds of the two tilings over the experts + 1 segments of m rows:
+// segments of up to 32 rows take at most two tiles; longer ones
+// ceil(rows / 64), i.e. at most m / 64 + (number of such segments <= m / 33).
+inline uint64_t small_tile_bound(int experts) { return 2 * ((uint64_t)experts + 1) + 1; }
+inline uint64_t big_tile_bound(uint64_t m, int experts) {
+    return m / 64 + std::min((uint64_t)experts + 1, m / 33) + 1;
+}
+
 struct PrefillWs {
-    uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, rows, parts, where_, Xhl, Hhl, P, end;
+    uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, rows, parts, where_, Xhl,
+        Hhl, P, end;
 };
 PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
     const uint64_t n = (uint64_t)tokens * topk, m = n + tokens;
@@ -599,7 +745,9 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
     w.offsets = up(w.dispatch + dispatch_workspace(tokens, experts));
     w.tiles_small = up(w.offsets + ((uint64_t)experts + 2) * 4);
     w.tiles_big = up(w.tiles_small + ((uint64_t)experts + 2) * 4);
-    w.rows = up(w.tiles_big + ((uint64_t)experts + 2) * 4);
+    w.info_small = up(w.tiles_big + ((uint64_t)experts + 2) * 4);
+    w.info_big = up(w.info_small + small_tile_bound(experts) * 16);
+    w.rows = up(w.info_big + big_tile_bound(m, experts) * 16);
     w.parts = up(w.rows + m * 4);
     w.where_ = up(w.parts + m * 4);
     w.Xhl = up(w.where_ + n * 4);
@@ -631,46 +779,60 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                               topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
                               (float *)(ws + w.gate)))
         return rc;
+    if (int rc = stage_mark(ctx, kStagePrefillDispatch)) return rc;
+    // The hi/lo split of the activations needs only X: it runs on the second
+    // stream beside the dispatch kernels, which occupy few CUs.
+    if (int rc = fork_aux(ctx)) return rc;
+    const int64_t groups = (int64_t)tokens * (width / 64);
+    k_split_hilo<<<(unsigned)((groups * 8 + 255) / 256), 256, 0, ctx->aux>>>((const float *)X,
+                                                                            (_Float16 *)(ws + w.Xhl), groups);
     int *offsets = (int *)(ws + w.offsets);
     int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);
-    if (int rc = stage_mark(ctx, kStagePrefillDispatch)) return rc;
-    const GemmTiling tiling = {tiles_small, tiles_big, 33, 32, 64};
-    if (int rc = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
-                                 (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, &tiling))
-        return rc;
-    const int64_t groups = (int64_t)tokens * (width / 64);
-    k_split_hilo<<<(unsigned)((groups * 64 + 255) / 256), 256, 0, ctx->stream>>>((const float *)X,
-                                                                               (_Float16 *)(ws + w.Xhl), groups);
-    if (int rc = launched(ctx)) return rc;
+    // Streaming kernels: N a multiple of 256 and K of 2048 or 512 in both
+    // products. Segments of up to 32 rows then run in 16-row tiles, else in
+    // one 32-row tile; longer ones in 64-row tiles.
+    const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && (width == 2048 || width == 512) &&
+                        (ff == 2048 || ff == 512);
+    const int4 *info_small = (const int4 *)(ws + w.info_small), *info_big = (const int4 *)(ws + w.info_big);
+    GemmTiling tiling = {tiles_small, tiles_big, 33, stream ? 16 : 32, 64};
+    tiling.info_small = (int *)info_small;
+    tiling.info_big = (int *)info_big;
+    int rc = launched(ctx);
+    if (rc == SM_OK)
+        rc = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
+                             (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, &tiling);
+    const int rc_join = join_aux(ctx);
+    if (rc) return rc;
+    if (rc_join) return rc_join;
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const uint64_t segs = (uint64_t)experts + 1;
     // Segment tilings: > 32 rows in 64-row tiles ("big"), <= 32 rows in one
     // 32-row tile ("small"). Wide blocks (big 64 x 512, small 32 x 1024, 8
     // waves) read each activation row once or twice; shapes whose N is not a
     // multiple of those widths use 4-wave 64 x 128 / 32 x 128 blocks.
-    const unsigned big_tiles = (unsigned)(m / 64 + std::min(segs, m / 33) + 1);
-    const unsigned small_tiles = (unsigned)(segs + 1);
+    const unsigned big_tiles = (unsigned)big_tile_bound(m, experts);
+    const unsigned small_tiles = (unsigned)(stream ? small_tile_bound(experts) : segs + 1);
     const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
     const int *rows = (const int *)(ws + w.rows);
     const uint8_t *ar = (const uint8_t *)arena, *sh = (const uint8_t *)shared_blob;
     auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
                      void *out, int ld) -> int {
-        if (N % 256 == 0 && (K == 2048 || K == 512)) {
+        if (stream) {
             auto kb = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 2, 2, 32> : k_moe_gemm_stream<true, 2, 2, 8>)
                               : (K == 2048 ? k_moe_gemm_stream<false, 2, 2, 32> : k_moe_gemm_stream<false, 2, 2, 8>);
             // The two tilings cover disjoint rows: the big-tile grid (few,
             // long blocks at small T) runs on the second stream beside the
             // small-tile grid.
             if (int rc = fork_aux(ctx)) return rc;
-            kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(a, r, offsets, tiles_big, ar, blob_stride,
+            kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(a, r, info_big, tiles_big, ar, blob_stride,
                                                                           sh, experts, codes, scales, K, N, out, ld);
             const int rc_big = launched(ctx);
-            auto ks = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 1, 2, 32> : k_moe_gemm_stream<true, 1, 2, 8>)
-                              : (K == 2048 ? k_moe_gemm_stream<false, 1, 2, 32> : k_moe_gemm_stream<false, 1, 2, 8>);
+            auto ks = gate_up ? (K == 2048 ? k_moe_gemm_stream16<true, 32> : k_moe_gemm_stream16<true, 8>)
+                              : (K == 2048 ? k_moe_gemm_stream16<false, 32> : k_moe_gemm_stream16<false, 8>);
             int rc_small = SM_OK;
             if (rc_big == SM_OK) {
                 ks<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
-                    a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+                    a, r, info_small, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
                 rc_small = launched(ctx);
             }
             const int rc_join = join_aux(ctx);
@@ -678,22 +840,22 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         }
         if (N % 512 == 0) {
             auto kb = gate_up ? k_moe_gemm<true, 2, 2, 1, 8> : k_moe_gemm<false, 2, 2, 1, 8>;
-            kb<<<dim3((unsigned)(N / 512), big_tiles), 512, 0, ctx->stream>>>(a, r, offsets, tiles_big, ar, blob_stride,
+            kb<<<dim3((unsigned)(N / 512), big_tiles), 512, 0, ctx->stream>>>(a, r, info_big, tiles_big, ar, blob_stride,
                                                                              sh, experts, codes, scales, K, N, out, ld);
         } else {
             auto kb = gate_up ? k_moe_gemm<true, 1, 2, 2, 2> : k_moe_gemm<false, 1, 2, 2, 2>;
-            kb<<<dim3((unsigned)(N / 128), big_tiles), 256, 0, ctx->stream>>>(a, r, offsets, tiles_big, ar, blob_stride,
+            kb<<<dim3((unsigned)(N / 128), big_tiles), 256, 0, ctx->stream>>>(a, r, info_big, tiles_big, ar, blob_stride,
                                                                              sh, experts, codes, scales, K, N, out, ld);
         }
         if (int rc = launched(ctx)) return rc;
         if (N % 1024 == 0) {
             auto ks = gate_up ? k_moe_gemm<true, 1, 4, 1, 8> : k_moe_gemm<false, 1, 4, 1, 8>;
             ks<<<dim3((unsigned)(N / 1024), small_tiles), 512, 0, ctx->stream>>>(
-                a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+                a, r, info_small, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
         } else {
             auto ks = gate_up ? k_moe_gemm<true, 1, 1, 1, 4> : k_moe_gemm<false, 1, 1, 1, 4>;
             ks<<<dim3((unsigned)(N / 128), small_tiles), 256, 0, ctx->stream>>>(
-                a, r, offsets, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+                a, r, info_small, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
         }
         return launched(ctx);
     };

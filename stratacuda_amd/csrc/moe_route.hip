@@ -85,34 +85,62 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
                                                     const float *__restrict__ bias, const float *__restrict__ Wsg,
                                                     float *__restrict__ logits, float *__restrict__ gate_out,
                                                     int tokens, int width, int experts, int with_gate) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nrows = experts + (with_gate ? 1 : 0);
     const int row_tiles = (nrows + TR - 1) / TR;
     const int tile = blockIdx.x * 4 + wave;
     if (tile >= row_tiles) return;
     const int r0 = tile * TR, t0 = blockIdx.y * TT;
-    const float *wp[TR];
-    const float *xp[TT];
+    // Row and token bases are the same for the whole wave (scalar registers);
+    // lanes differ only by a 32-bit byte offset.
+    const char *wp[TR];
+    const char *xp[TT];
 #pragma unroll
     for (int r = 0; r < TR; r++) {
         int row = min(r0 + r, nrows - 1);
-        wp[r] = row < experts ? Wr + (int64_t)row * width : Wsg;
+        wp[r] = (const char *)(row < experts ? Wr + (int64_t)row * width : Wsg);
     }
 #pragma unroll
-    for (int t = 0; t < TT; t++) xp[t] = X + (int64_t)min(t0 + t, tokens - 1) * width;
+    for (int t = 0; t < TT; t++) xp[t] = (const char *)(X + (int64_t)min(t0 + t, tokens - 1) * width);
     float a[64];
 #pragma unroll
     for (int o = 0; o < 64; o++) a[o] = 0.0f;
-    for (int i = lane; i < width; i += 64) {
-        float xv[TT], wv[TR];
+    float xv[TT], wv[TR];
+    auto load = [&](uint32_t off, float *xd, float *wd) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < TT; t++) xv[t] = xp[t][i];
+        for (int t = 0; t < TT; t++) xd[t] = *(const float *)(xp[t] + off);
 #pragma unroll
-        for (int r = 0; r < TR; r++) wv[r] = wp[r][i];
+        for (int r = 0; r < TR; r++) wd[r] = *(const float *)(wp[r] + off);
+    };
+    auto madd = [&](const float *xs, const float *ws) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int r = 0; r < TR; r++) a[t * TR + r] = a[t * TR + r] + wv[r] * xv[t];
+            for (int r = 0; r < TR; r++) a[t * TR + r] = a[t * TR + r] + ws[r] * xs[t];
+    };
+    if (width % 64 == 0) {
+        // Each lane sums its positions lane, lane + 64, ... in order; the next
+        // position's values are loaded while the current ones are used. The
+        // loads are unconditional (past the end they repeat the last
+        // position), so the compiler's waits only cover the buffer in use.
+        const int steps = width / 64;
+        const uint32_t first = (uint32_t)lane * 4u, last = first + (uint32_t)(steps - 1) * 256u;
+        uint32_t off = first;
+        float xn[TT], wn[TR];
+        load(off, xv, wv);
+        for (int k = 0;; k += 2, off += 512u) {
+            load(min(off + 256u, last), xn, wn);
+            madd(xv, wv);
+            if (k + 1 >= steps) break;
+            load(min(off + 512u, last), xv, wv);
+            madd(xn, wn);
+            if (k + 2 >= steps) break;
+        }
+    } else {
+        for (int i = lane; i < width; i += 64) {
+            load((uint32_t)i * 4u, xv, wv);
+            madd(xv, wv);
+        }
     }
     butterfly_level<64>(a, lane);
     butterfly_level<32>(a, lane);
@@ -141,103 +169,135 @@ __global__ void __launch_bounds__(256) k_topk(const float *__restrict__ logits, 
 
 // ---------------------------------------------------------------- dispatch
 // Block b covers tokens [64b, 64b+64). masks[b*E + e] = tokens of the block
-// routed to e; counts[e*nb + b] = popcount. status bit 0: an ID outside
-// [0, experts); bit 1: an ID repeated within one token.
+// routed to e; counts[b*E + e] = popcount; flags[b] bit 0: an ID outside
+// [0, experts) (left out, marked by k_dispatch_place), bit 1: an ID repeated
+// within one token. k_dispatch_scan folds the flags into the status word.
 __global__ void __launch_bounds__(256) k_dispatch_masks(const int *__restrict__ ids, int tokens, int topk, int experts,
                                                         int nb, unsigned long long *__restrict__ masks,
-                                                        int *__restrict__ counts, uint32_t *status) {
+                                                        int *__restrict__ counts, uint32_t *__restrict__ flags) {
     __shared__ unsigned long long m[512];
+    __shared__ uint32_t s_flags;
     const int b = blockIdx.x;
     for (int e = threadIdx.x; e < experts; e += blockDim.x) m[e] = 0ull;
+    if (threadIdx.x == 0) s_flags = 0;
     __syncthreads();
     const int t0 = b * 64, nt = min(64, tokens - t0);
     for (int a = threadIdx.x; a < nt * topk; a += blockDim.x) {
         int tl = a / topk, e = ids[(int64_t)(t0 + tl) * topk + a % topk];
         if (e < 0 || e >= experts) {
-            atomicOr(status, 1u);
+            atomicOr(&s_flags, 1u);
             continue;
         }
-        unsigned long long bit = 1ull << tl;
-        unsigned long long old = atomicOr(&m[e], bit);
-        if (old & bit) atomicOr(status, 2u);
+        const unsigned long long bit = 1ull << tl;
+        if (atomicOr(&m[e], bit) & bit) atomicOr(&s_flags, 2u);
     }
     __syncthreads();
     for (int e = threadIdx.x; e < experts; e += blockDim.x) {
         masks[(int64_t)b * experts + e] = m[e];
-        counts[(int64_t)e * nb + b] = __popcll(m[e]);
+        counts[(int64_t)b * experts + e] = __popcll(m[e]);
     }
+    if (threadIdx.x == 0) flags[b] = s_flags;
 }
 
-// Single block: exclusive scan of counts (expert-major) into base, per-expert
-// offsets[E+1] (+ offsets[E+1] = offsets[E] + extra for the shared-expert
-// segment), and the m-tile bases of the grouped GEMMs over the E+1 segments:
-// a segment with at least `split` rows is tiled by mt_big rows in tile_big
-// and is absent from tile_small, a shorter one the other way round
-// (tile_x[s] = tiles of the segments before s; tile_x[E+1] = the total).
-__global__ void __launch_bounds__(1024) k_dispatch_scan(const int *__restrict__ counts, int *__restrict__ base,
-                                                        int *__restrict__ offsets, int *__restrict__ tile_small,
-                                                        int *__restrict__ tile_big, int experts, int nb, int extra,
-                                                        int split, int mt_small, int mt_big) {
-    __shared__ int part[1024];
-    __shared__ int tsm[1024], tbg[1024];
-    const int n = experts * nb, tid = threadIdx.x;
-    const int chunk = (n + 1023) / 1024, lo = min(n, tid * chunk), hi = min(n, lo + chunk);
-    int s = 0;
-    for (int b0 = lo; b0 < hi; b0 += 8) {  // 8 loads in flight at a time
-        int v[8];
+// Inclusive prefix sum over one block of SCAN_THREADS threads (wave scans,
+// then the wave totals). s_wave holds SCAN_THREADS / 64 ints.
+constexpr int SCAN_THREADS = 1024;
+__device__ __forceinline__ int block_inclusive_scan(int v, int *s_wave) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = b0 + u < hi ? counts[b0 + u] : 0;
-#pragma unroll
-        for (int u = 0; u < 8; u++) s += v[u];
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
     }
-    part[tid] = s;
+    if (lane == 63) s_wave[wave] = v;
     __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        int v = tid >= d ? part[tid - d] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; w++) before += s_wave[w];
+    __syncthreads();  // s_wave may be reused by the next scan
+    return v + before;
+}
+
+// Single block, one thread per expert: the expert's total over the token
+// blocks (counts[b*E + e]: each step reads one contiguous row), the exclusive scan of the totals in expert order (offsets[E];
+// offsets[E+1] = offsets[E] + extra for the shared-expert segment), the
+// per-block bases (base[b*E + e] = offsets[e] + counts of e in blocks < b),
+// and the m-tile bases of the grouped GEMMs over the E+1 segments: a segment
+// with at least `split` rows is tiled by mt_big rows in tile_big and is
+// absent from tile_small, a shorter one the other way round (tile_x[s] =
+// tiles of the segments before s; tile_x[E+1] = the total). experts < 1024.
+__global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_scan(const int *__restrict__ counts, int *__restrict__ base,
+                                                                int *__restrict__ offsets, int *__restrict__ tile_small,
+                                                                int *__restrict__ tile_big, int experts, int nb, int extra,
+                                                                int split, int mt_small, int mt_big,
+                                                                const uint32_t *__restrict__ flags,
+                                                                uint32_t *__restrict__ status,
+                                                                int4 *__restrict__ info_small,
+                                                                int4 *__restrict__ info_big) {
+    __shared__ int s_wave[SCAN_THREADS / 64];
+    __shared__ uint32_t s_status;
+    const int e = threadIdx.x;
+    if (e == 0) s_status = 0;
+    __syncthreads();
+    for (int b = e; b < nb; b += SCAN_THREADS)
+        if (flags[b]) atomicOr(&s_status, flags[b]);
+    // The column is read in batches of SCAN_BATCH independent loads (one
+    // batch up to 2048 tokens); a batch is kept for the base pass when it is
+    // the only one.
+    constexpr int SCAN_BATCH = 32;
+    const int ec = min(e, experts - 1);  // threads past the experts read a valid column
+    int v[SCAN_BATCH];
+    int tot = 0;
+    for (int b0 = 0; b0 < nb; b0 += SCAN_BATCH) {
+#pragma unroll
+        for (int u = 0; u < SCAN_BATCH; u++) v[u] = counts[(int64_t)min(b0 + u, nb - 1) * experts + ec];
+#pragma unroll
+        for (int u = 0; u < SCAN_BATCH; u++) tot += b0 + u < nb ? v[u] : 0;
     }
-    int run = tid ? part[tid - 1] : 0;
-    for (int b0 = lo; b0 < hi; b0 += 8) {
-        int v[8];
+    if (e >= experts) tot = 0;
+    const int incl = block_inclusive_scan(tot, s_wave), excl = incl - tot;
+    if (e < experts) {
+        offsets[e] = excl;
+        int run = excl;
+        for (int b0 = 0; b0 < nb; b0 += SCAN_BATCH) {
+            if (nb > SCAN_BATCH) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = b0 + u < hi ? counts[b0 + u] : 0;
+                for (int u = 0; u < SCAN_BATCH; u++) v[u] = counts[(int64_t)min(b0 + u, nb - 1) * experts + e];
+            }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            if (b0 + u < hi) base[b0 + u] = run;
-            run += v[u];
+            for (int u = 0; u < SCAN_BATCH; u++)
+                if (b0 + u < nb) {
+                    base[(int64_t)(b0 + u) * experts + e] = run;
+                    run += v[u];
+                }
+        }
+        if (e == experts - 1) {
+            offsets[experts] = incl;
+            offsets[experts + 1] = incl + extra;
         }
     }
-    __syncthreads();
-    const int total = part[1023];
-    for (int e = tid; e < experts; e += 1024) offsets[e] = base[(int64_t)e * nb];
-    if (tid == 0) {
-        offsets[experts] = total;
-        offsets[experts + 1] = total + extra;
-    }
-    __syncthreads();
-    // Tiles per segment (experts + 1 segments, the last may be empty), then an
-    // inclusive scan of each kind; experts + 1 <= 513 < 1024.
+    // Tiles per segment (experts + 1 segments; the last holds the extra rows
+    // and may be empty), then an inclusive scan of each kind.
+    const int cnt = e < experts ? tot : e == experts ? extra : 0;
     int ns = 0, nbg = 0;
-    if (tid <= experts) {
-        const int cnt = offsets[tid + 1] - offsets[tid];
-        if (cnt >= split) nbg = (cnt + mt_big - 1) / mt_big;
-        else ns = (cnt + mt_small - 1) / mt_small;
+    if (cnt >= split) nbg = (cnt + mt_big - 1) / mt_big;
+    else ns = (cnt + mt_small - 1) / mt_small;
+    const int ts = block_inclusive_scan(ns, s_wave), tb = block_inclusive_scan(nbg, s_wave);
+    if (e == 0) *status = s_status;  // block scans above synchronised the block
+    // Tile records of the segment (excl is the segment's first row, also for
+    // the shared-expert segment, whose total is 0 here).
+    if (e <= experts) {
+        int4 *info = ns ? info_small : info_big;
+        const int n = ns ? ns : nbg, mt = ns ? mt_small : mt_big, first = (ns ? ts : tb) - n;
+        if (info)
+            for (int j = 0; j < n; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, 0);
     }
-    tsm[tid] = ns;
-    tbg[tid] = nbg;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        int vs = tid >= d ? tsm[tid - d] : 0, vb = tid >= d ? tbg[tid - d] : 0;
-        __syncthreads();
-        tsm[tid] += vs;
-        tbg[tid] += vb;
-        __syncthreads();
-    }
-    if (tid <= experts + 1) {
-        if (tile_small) tile_small[tid] = tid ? tsm[tid - 1] : 0;
-        if (tile_big) tile_big[tid] = tid ? tbg[tid - 1] : 0;
+    if (e <= experts) {
+        if (tile_small) tile_small[e + 1] = ts;
+        if (tile_big) tile_big[e + 1] = tb;
+        if (e == 0) {
+            if (tile_small) tile_small[0] = 0;
+            if (tile_big) tile_big[0] = 0;
+        }
     }
 }
 
@@ -255,7 +315,7 @@ __global__ void k_dispatch_place(const int *__restrict__ ids, int tokens, int to
         }
         int b = t >> 6, tl = t & 63;
         unsigned long long below = tl ? (masks[(int64_t)b * experts + e] & ((1ull << tl) - 1ull)) : 0ull;
-        int pos = base[(int64_t)e * nb + b] + __popcll(below);
+        int pos = base[(int64_t)b * experts + e] + __popcll(below);
         rows[pos] = t;
         parts[pos] = (int)a;
         where_[a] = pos;
@@ -272,13 +332,14 @@ constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct DispatchWs {
-    uint64_t status, masks, counts, base, tile_small, tile_big, end;
+    uint64_t status, flags, masks, counts, base, tile_small, tile_big, end;
 };
 DispatchWs dispatch_ws(int tokens, int experts) {
     const uint64_t nb = (uint64_t)(tokens + 63) / 64;
     DispatchWs w;
-    w.status = 0;
-    w.masks = up(w.status + 64);
+    w.status = 0;  // uint32: bit 0 an ID out of range, bit 1 an ID repeated within a token
+    w.flags = up(w.status + 64);
+    w.masks = up(w.flags + (uint64_t)nb * 4);
     w.counts = up(w.masks + nb * experts * 8);
     w.base = up(w.counts + nb * experts * 4);
     w.tile_small = up(w.base + nb * experts * 4);
@@ -348,15 +409,16 @@ int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int exper
     const int nb = ceil_div(tokens, 64);
     DispatchWs w = dispatch_ws(tokens, experts);
     const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
-    if (int rc = zero_words(ctx, ws + w.status, 16)) return rc;
     k_dispatch_masks<<<nb, 256, 0, ctx->stream>>>(ids, tokens, topk, experts, nb, (unsigned long long *)(ws + w.masks),
-                                                  (int *)(ws + w.counts), (uint32_t *)(ws + w.status));
+                                                  (int *)(ws + w.counts), (uint32_t *)(ws + w.flags));
     if (int rc = launched(ctx)) return rc;
     GemmTiling none = {(int *)(ws + w.tile_small), (int *)(ws + w.tile_big), 64, 32, 128};
     const GemmTiling &tl = tiling ? *tiling : none;
-    k_dispatch_scan<<<1, 1024, 0, ctx->stream>>>((const int *)(ws + w.counts), (int *)(ws + w.base), offsets,
+    k_dispatch_scan<<<1, SCAN_THREADS, 0, ctx->stream>>>((const int *)(ws + w.counts), (int *)(ws + w.base), offsets,
                                                  tl.small, tl.big, experts, nb, (int)extra, tl.split, tl.mt_small,
-                                                 tl.mt_big);
+                                                 tl.mt_big, (const uint32_t *)(ws + w.flags),
+                                                 (uint32_t *)(ws + w.status), (int4 *)tl.info_small,
+                                                 (int4 *)tl.info_big);
     if (int rc = launched(ctx)) return rc;
     const uint64_t threads = n + extra;
     k_dispatch_place<<<(unsigned)((threads + 255) / 256), 256, 0, ctx->stream>>>(
