@@ -95,7 +95,7 @@ def cpu_baseline(oracle, wl, seconds):
 
 PROFILE_CMDS = {
     "trace": "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/trace -o decode -- "
-             "python3 -u bench.py --no-cpu --eager --steps 960",
+             "python3 -u bench.py --no-cpu --eager --no-stack --steps 960",
     "fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o decode -- "
              "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --layers 8 --steps 16 --warmup 8",
     "write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o decode -- "
@@ -141,6 +141,13 @@ def _gemm_label(name):
     if m:
         return "k_moe_gemm_stream<%s, %d x %d tile, K/64 = %s>" % (
             "gate_up" if m.group(1) == "1" else "down", 32 * int(m.group(2)), 128 * int(m.group(3)), m.group(4))
+    m = re.search(r"k_moe_gemm_stream16ILb(\d)ELi(\d+)E", name)
+    if m:
+        return "k_moe_gemm_stream16<%s, 16 x 256 tile, K/64 = %s>" % ("gate_up" if m.group(1) == "1" else "down",
+                                                                     m.group(2))
+    m = re.search(r"k_split_hilo", name)
+    if m:
+        return "k_split_hilo"
     return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
 
 
@@ -196,7 +203,7 @@ def summarize(out_dir):
              "Command (from the repository root):", "", "    " + PROFILE_CMDS["trace"], "",
              "| kernel | calls | avg us | min us | max us | share |", "|---|---|---|---|---|---|"]
     for r in _csv_rows(stats[0]):
-        name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        name = _gemm_label(r["Name"])
         lines.append("| %s | %s | %.3f | %.3f | %.3f | %s%% |" % (
             name, r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
             r["Percentage"]))

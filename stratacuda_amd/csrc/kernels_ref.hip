@@ -166,16 +166,35 @@ __global__ void k_norm(const float *X, const float *W, float *Y, int cols, int r
     if (!logical_group(total, g)) return;
     int row = (int)g, lane = lane_id();
     if (row >= rows) return;
+    // Lane-strided sum of squares in the reference order; the loads go out
+    // eight at a time so their latencies overlap.
+    const float *xr = X + (int64_t)row * cols;
     float ss = 0.0f;
-    for (int i = lane; i < cols; i += 64) {
-        float v = X[(int64_t)row * cols + i];
-        ss = ss + v * v;
+    for (int i0 = lane; i0 < cols; i0 += 8 * 64) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = xr[min(i0 + 64 * u, cols - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + 64 * u < cols) ss = ss + v[u] * v[u];
     }
     ss = __shfl(sm::tree_sum64(ss), 0, 64);
     float inv = scale / sqrtf((mode == 0 ? ss / (float)cols : ss) + epsilon);
-    for (int i = lane; i < cols; i += 64) {
-        float w = mode == 0 ? W[(int64_t)(row % weightRows) * cols + i] : 1.0f;
-        Y[(int64_t)row * cols + i] = X[(int64_t)row * cols + i] * inv * w;
+    // Eight positions per lane are loaded before any is stored (Y may alias
+    // X, and without the batching every store would wait for the next load).
+    const float *wr = W + (int64_t)(row % weightRows) * cols;
+    float *yr = Y + (int64_t)row * cols;
+    for (int i0 = lane; i0 < cols; i0 += 8 * 64) {
+        float x[8], w[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = min(i0 + 64 * u, cols - 1);
+            x[u] = xr[i];
+            w[u] = mode == 0 ? wr[i] : 1.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + 64 * u < cols) yr[i0 + 64 * u] = x[u] * inv * w[u];
     }
 }
 
