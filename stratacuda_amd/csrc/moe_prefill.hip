@@ -9,14 +9,14 @@
 //   combine   Y[t] = P[shared(t)] * sigmoid(gate_t) + sum_k P[where(t,k)] * w_tk
 //             in the reference order (kernels/strata.cu:470-476)
 //
-// Grouped GEMM on MFMA (v_mfma_f32_32x32x16_f16, f32 accumulation):
+// Grouped GEMM on MFMA (fp16 operands, f32 accumulation):
 //  * Weights: (code - 1) * fp16 scale is exactly representable in fp16, so the
-//    B operand holds the exact reference weights. Codes become fp16 pairs with
-//    one mask ((w >> 2p) & 0x00030003 puts codes p and p+8 of a 16-code word
-//    into the two halves), an OR with the exponent pattern of 1024 (0x6400), a
-//    packed subtract of 1025 and a packed multiply by the group scale; all
-//    three steps are exact. Each wave dequantises its own B fragments in
-//    registers, once per K step, and uses each for 2 * MI MFMAs.
+//    B operand holds the exact reference weights. In the streaming kernels a
+//    pair of codes becomes an fp16 pair in three exact steps: one AND-OR puts
+//    the two 2-bit codes under an fp16 exponent that makes each the units
+//    digit (no shift per pair), a packed subtract leaves c - 1, a packed
+//    multiply applies the group scale. Each wave dequantises its own B
+//    fragments in registers once per K step.
 //  * Activations are split once into hi = fp16(x) and lo = fp16(x - hi) (the
 //    gate/up input by k_split_hilo, the down input by the gate/up epilogue);
 //    two MFMAs (hi and lo) per K step give products accurate to ~2^-22
@@ -27,13 +27,15 @@
 //    (p, p+8) of word w come out of the code unpacking, so B needs no
 //    shuffle; the activations are stored in the same order, so staging them
 //    into LDS is a plain 16-byte copy and the MFMA A operand one 16-byte read.
-//  * Tiles: each wave MI x NI MFMA tiles of 32 x 32. Segments of more than 32
-//    rows run in 64-row tiles with 64 x 512 blocks (8 waves of 64 x 64),
-//    shorter ones in one 32-row tile with 32 x 1024 blocks (8 waves of
-//    32 x 128), in two launches, so each activation row is read from memory
-//    once or twice per GEMM; the A tile (hi and lo) is staged in LDS per scale
-//    group, double-buffered, with the next group's A and B loads in flight
-//    during the current MFMAs.
+//  * Tiles (width and ff among 512 / 2048, the benchmark shapes): segments of
+//    more than 32 rows run in 64 x 256 blocks on v_mfma_f32_32x32x16_f16
+//    (k_moe_gemm_stream), shorter ones in 16 x 256 blocks on
+//    v_mfma_f32_16x16x32_f16 (k_moe_gemm_stream16); the two grids cover
+//    disjoint rows and run on two streams. Both stream A and B through a ring
+//    of LDS stages filled by direct global->LDS loads. Each block reads its
+//    tile record (segment, first row, end row) written by the dispatch.
+//    Other shapes use k_moe_gemm (register-held B, A double-buffered in LDS,
+//    64- and 32-row tiles).
 //    grid.x = n-block (fastest) so the m-tiles of one (expert, n-block) run
 //    on one XCD and share its L2.
 #include <hip/hip_runtime.h>
@@ -806,10 +808,8 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     if (rc_join) return rc_join;
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const uint64_t segs = (uint64_t)experts + 1;
-    // Segment tilings: > 32 rows in 64-row tiles ("big"), <= 32 rows in one
-    // 32-row tile ("small"). Wide blocks (big 64 x 512, small 32 x 1024, 8
-    // waves) read each activation row once or twice; shapes whose N is not a
-    // multiple of those widths use 4-wave 64 x 128 / 32 x 128 blocks.
+    // Segment tilings: > 32 rows in 64-row tiles ("big"), <= 32 rows in
+    // 16-row tiles (streaming kernels) or one 32-row tile (k_moe_gemm).
     const unsigned big_tiles = (unsigned)big_tile_bound(m, experts);
     const unsigned small_tiles = (unsigned)(stream ? small_tile_bound(experts) : segs + 1);
     const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
