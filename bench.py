@@ -108,8 +108,10 @@ for _case in ("512", "2048zipf"):
         "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_BUSY_CYCLES GRBM_GUI_ACTIVE "
         "-f csv -d gpurun_out/pmc_mfma_%s -o prefill -- python3 -u bench.py --no-cpu --eager --no-stack --layers 2 "
         "--steps 2 --warmup 2 --prefill-reps 4 --prefill-cases %s" % (_case, _case))
-MFMA_FLOP_PER_INST = 2 * 32 * 32 * 16   # v_mfma_f32_32x32x16_f16, the only MFMA the prefill kernels issue
-MFMA_CYCLES_PER_INST = 32               # busy cycles per such instruction on one SIMD
+# FLOPs per MFMA instruction: v_mfma_f32_32x32x16_f16 (64-row and register-B
+# kernels), v_mfma_f32_16x16x32_f16 (16-row kernels).
+MFMA_FLOP_32 = 2 * 32 * 32 * 16
+MFMA_FLOP_16 = 2 * 16 * 16 * 32
 SIMDS = 256 * 4
 DECODE_KERNELS = ["k_decode_route", "k_decode_gate_up", "k_decode_down"]
 
@@ -170,10 +172,11 @@ def summarize_mfma(path, case, dest):
         agg.setdefault(_gemm_label(d["name"]), []).append(d)
     lines = ["# MFMA use of the prefill kernels, T=%s" % case.replace("zipf", " (Zipf-biased router)"), "",
              "Command (from the repository root):", "", "    " + PROFILE_CMDS["mfma_" + case], "",
-             "Issued rate = SQ_INSTS_MFMA x %d FLOP / duration (each algorithmic product runs twice, once for the "
-             "high and once for the low fp16 half of the activations, so the algorithmic rate is half of it). "
-             "Busy = SQ_VALU_MFMA_BUSY_CYCLES / (%d SIMDs x duration x 2.4 GHz). Peak: 2.5 PFLOP/s dense fp16."
-             % (MFMA_FLOP_PER_INST, SIMDS), "",
+             "Issued rate = SQ_INSTS_MFMA x FLOP per instruction (%d for the 32x32x16 MFMA of the 64-row tiles, "
+             "%d for the 16x16x32 MFMA of the 16-row tiles) / duration; each algorithmic product runs twice, "
+             "once for the high and once for the low fp16 half of the activations, so the algorithmic rate is half "
+             "of it. Busy = SQ_VALU_MFMA_BUSY_CYCLES / (%d SIMDs x duration x 2.4 GHz). Peak: 2.5 PFLOP/s dense fp16."
+             % (MFMA_FLOP_32, MFMA_FLOP_16, SIMDS), "",
              "| kernel | dispatches | avg us | MFMA insts | issued TFLOP/s | issued / peak | MFMA busy | VALU insts |",
              "|---|---|---|---|---|---|---|---|"]
     for name, ds in agg.items():
@@ -182,7 +185,7 @@ def summarize_mfma(path, case, dest):
         mf = sum(d.get("SQ_INSTS_MFMA", 0) for d in ds) / n
         busy = sum(d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) for d in ds) / n
         va = sum(d.get("SQ_INSTS_VALU", 0) for d in ds) / n
-        rate = mf * MFMA_FLOP_PER_INST / (us * 1e-6) / 1e12 if us else 0.0
+        rate = mf * (MFMA_FLOP_16 if "stream16" in name else MFMA_FLOP_32) / (us * 1e-6) / 1e12 if us else 0.0
         lines.append("| %s | %d | %.1f | %.0f | %.1f | %.3f | %.3f | %.0f |" % (
             name, n, us, mf, rate, rate * 1e12 / PEAK_MFMA_F16, busy / (SIMDS * us * 1e-6 * 2.4e9) if us else 0.0,
             va))
