@@ -60,6 +60,12 @@ __device__ __forceinline__ float dot64(uint4 c, const float *x) {
     b = dot16(c.w, x + 48, b);
     return a + b;
 }
+// The same with four independent chains (one per code word).
+__device__ __forceinline__ float dot64_4(uint4 c, const float *x) {
+    const float a = dot16(c.x, x, 0.0f), b = dot16(c.y, x + 16, 0.0f);
+    const float d = dot16(c.z, x + 32, 0.0f), e = dot16(c.w, x + 48, 0.0f);
+    return (a + b) + (d + e);
+}
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // One 16-byte code group, streamed (non-temporal: weights are read once).
@@ -325,56 +331,99 @@ __device__ __forceinline__ void down_combine(const float *parts, const float *__
 }
 
 // K3 for ff <= 512 (one 64-value group per lane). Grid ceil(width / 8),
-// 256 threads, 8 output rows per block. Wave w handles slots w, w+4, ...;
-// lane (r = lane / 8, gl = lane % 8) dots group gl of down row r with group gl
-// of the slot's hidden vector. The slot IDs are wave-uniform scalar loads;
-// every code group of the wave is requested before any arithmetic, and each
-// slot's hidden group is loaded as its turn comes. Partial rows meet in LDS
-// for the combine.
-constexpr int DN_MAX_SLOTS = 9;  // slots per wave (33 slots / 4 waves)
-__global__ void __launch_bounds__(256) k_decode_down(const float *__restrict__ hidden, const uint8_t *__restrict__ arena,
-                                                     uint64_t stride, const uint8_t *__restrict__ shared_blob,
-                                                     const int *__restrict__ ids, const float *__restrict__ weights,
-                                                     const float *__restrict__ gate, float *__restrict__ Y, int width,
-                                                     int ff, int topk, int experts, uint64_t down_codes,
-                                                     uint64_t down_scales) {
+// 512 threads, 8 output rows per block. Wave w handles slots w, w+8, ...;
+// lane (r = lane / 8, gl = lane % 8) dots group gl of down row r with group
+// gl of the slot's hidden vector. The 8 lanes that need the same hidden
+// group each load an eighth of it and pass it on through a wave-private LDS
+// area (every hidden value is read from memory once per wave, not 8 times);
+// the same 8 lanes form the group's sum with three cross-lane adds. Slot IDs
+// are one vector load read back per slot with v_readlane; loads go out on
+// clamped addresses without branches, so each wait covers only what it
+// needs. Partial rows meet in LDS for the combine.
+constexpr int DN_WAVES = 8;
+constexpr int DN_MAX_SLOTS = 5;  // slots per wave (33 slots / 8 waves)
+constexpr int DN_PITCH = 68;     // floats per group in the exchange area (16-byte skew per group)
+template <int NQ>  // slots per wave: ceil((topk + 1) / DN_WAVES)
+__global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__restrict__ hidden,
+                                                              const uint8_t *__restrict__ arena, uint64_t stride,
+                                                              const uint8_t *__restrict__ shared_blob,
+                                                              const int *__restrict__ ids,
+                                                              const float *__restrict__ weights,
+                                                              const float *__restrict__ gate, float *__restrict__ Y,
+                                                              int width, int ff, int topk, int experts,
+                                                              uint64_t down_codes, uint64_t down_scales) {
+    static_assert(NQ >= 1 && NQ <= DN_MAX_SLOTS, "slots per wave");
     __shared__ float parts[33 * 8];
     __shared__ uint64_t s_tab[32];
+    __shared__ __attribute__((aligned(16))) float s_h[DN_WAVES][8 * DN_PITCH];
     const int nexp = topk + 1, GF = ff / 64;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r = min((int)blockIdx.x * 8 + (lane >> 3), width - 1), gl = lane & 7;
+    const int rr = lane >> 3, gl = lane & 7;
+    const int r = min((int)blockIdx.x * 8 + rr, width - 1);
+    const int gc = min(gl, GF - 1);
     const uint64_t row_bytes = (uint64_t)ff / 4;
-    uint4 c[DN_MAX_SLOTS];
-    uint32_t sb[DN_MAX_SLOTS];
-    const uint8_t *blobs[DN_MAX_SLOTS];
+    const int my_id = ids[min(lane, topk - 1)];
+    // The lane's eighth (8 values) of its hidden group, for every slot.
+    float4 hq[NQ][2];
 #pragma unroll
-    for (int q = 0; q < DN_MAX_SLOTS; q++) {
-        const int k = wave + 4 * q;
-        blobs[q] = nullptr;
-        c[q] = make_uint4(0, 0, 0, 0);
-        sb[q] = 0;
-        if (k < nexp) {
-            blobs[q] = slot_blob(arena, stride, shared_blob, k < topk ? ids[k] : 0, k, topk, experts);
-            if (blobs[q] && gl < GF) {
-                c[q] = load_codes(blobs[q] + down_codes + (uint64_t)r * row_bytes + (uint64_t)gl * 16);
-                sb[q] = *(const uint16_t *)(blobs[q] + down_scales + ((uint64_t)r * GF + gl) * 2);
-            }
-        }
+    for (int q = 0; q < NQ; q++) {
+        const float *src = hidden + (uint64_t)min(wave + DN_WAVES * q, nexp - 1) * ff + gc * 64 + 8 * rr;
+        hq[q][0] = *(const float4 *)src;
+        hq[q][1] = *(const float4 *)(src + 4);
+    }
+    uint4 c[NQ];
+    uint32_t sb[NQ];
+    bool ok[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const int k = wave + DN_WAVES * q;
+        const int lid = __builtin_amdgcn_readlane(my_id, min(k, 63));
+        const int id = k < topk ? lid : 0;
+        const uint8_t *blob = k < nexp ? slot_blob(arena, stride, shared_blob, id, k, topk, experts) : shared_blob;
+        ok[q] = blob != nullptr;
+        blob = blob ? blob : shared_blob;  // an invalid ID reads the shared blob; the slot yields NaN
+        c[q] = load_codes(blob + down_codes + (uint64_t)r * row_bytes + (uint64_t)gc * 16);
+        sb[q] = *(const uint16_t *)(blob + down_scales + ((uint64_t)r * GF + gc) * 2);
     }
     sm::fill_exp_table(s_tab);
+    float *xh = s_h[wave];
 #pragma unroll
-    for (int q = 0; q < DN_MAX_SLOTS; q++) {
-        const int k = wave + 4 * q;
-        if (k >= nexp) break;
-        float v = blobs[q] ? 0.0f : __builtin_nanf("");
-        if (blobs[q] && gl < GF) {
-            float h[64];
-            load_group(hidden + (uint64_t)k * ff + gl * 64, h);
-            v = sm::half_bits(sb[q]) * (dot64(c[q], h) - sum64(h));
+    for (int q = 0; q < NQ; q++) {
+        const int k = wave + DN_WAVES * q;
+        // group sum: own eighth, then over the lanes gl + 8j: lane ^ 8
+        // (row_ror:8 inside a 16-lane row), lane ^ 16 and lane ^ 32 (the two
+        // results of a v_permlane16/32_swap of a value with itself hold, in
+        // every lane, the lane's own value and its partner's).
+        const float4 a = hq[q][0], b = hq[q][1];
+        float s8 = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+        s8 = s8 + sm::dpp_f32<0x128>(0.0f, s8);
+        {
+            const int u = __builtin_bit_cast(int, s8);
+            const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            s8 = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
+            const int w = __builtin_bit_cast(int, s8);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+            s8 = __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
         }
+        // exchange: lane (rr, gl) stores values 8 rr .. 8 rr + 7 of group gl
+        *(float4 *)&xh[gl * DN_PITCH + 8 * rr] = a;
+        *(float4 *)&xh[gl * DN_PITCH + 8 * rr + 4] = b;
+        __builtin_amdgcn_wave_barrier();
+        float h[64];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = *(const float4 *)&xh[gl * DN_PITCH + 4 * i];
+            h[4 * i] = v.x;
+            h[4 * i + 1] = v.y;
+            h[4 * i + 2] = v.z;
+            h[4 * i + 3] = v.w;
+        }
+        __builtin_amdgcn_wave_barrier();
+        float v = ok[q] ? 0.0f : __builtin_nanf("");
+        if (ok[q] && gl < GF) v = sm::half_bits(sb[q]) * (dot64_4(c[q], h) - s8);
         v = sm::group8_sum(v);
-        if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
+        if (gl == 0 && k < nexp) parts[k * 8 + rr] = v;
     }
     __syncthreads();
     down_combine(parts, weights, gate, Y, width, topk, s_tab);
@@ -474,8 +523,13 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
     // 3. down for all experts + combine
     if (stage_on(ctx, kStageDecodeDown)) {
         if (int rc = stage_mark(ctx, kStageDecodeDown)) return rc;
-        auto kernel = ff <= 512 ? k_decode_down : k_decode_down_wide;
-        kernel<<<(unsigned)ceil_div(width, 8), 256, 0, ctx->stream>>>(
+        using K3 = void (*)(const float *, const uint8_t *, uint64_t, const uint8_t *, const int *, const float *,
+                            const float *, float *, int, int, int, int, uint64_t, uint64_t);
+        static const K3 by_slots[DN_MAX_SLOTS] = {k_decode_down<1>, k_decode_down<2>, k_decode_down<3>,
+                                                  k_decode_down<4>, k_decode_down<5>};
+        const bool narrow = ff <= 512;
+        const K3 kernel = narrow ? by_slots[ceil_div(topk + 1, DN_WAVES) - 1] : k_decode_down_wide;
+        kernel<<<(unsigned)ceil_div(width, 8), narrow ? 64 * DN_WAVES : 256, 0, ctx->stream>>>(
             hidden, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const int *)ids,
             (const float *)weights, (const float *)(ws + w.gate), (float *)Y, width, ff, topk, experts, L.down_codes,
             L.down_scales);
