@@ -125,6 +125,23 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
                  int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,
                  uint64_t workspace_bytes);
 
+/* One block of a stacked decoder built on the MoE stage, the per-layer step
+ * of the 48-layer stack (no single reference entry point; it composes
+ * strata_norm mode 0 with scale 1, kernels/strata.cu:214-227, the MoE stage of
+ * sm_moe_layer, and strata_elementwise mode 5, :230-236):
+ *   Hout = H + MoE(RMSNorm(H; gamma, eps))          per token.
+ * gamma is [width] f32. Results are bit-identical to running those three
+ * steps separately. tokens == 1 folds the normalisation into the router
+ * kernel and the residual into the down kernel; tokens > 1 normalises into
+ * the workspace and adds the residual in the combine. Hout may be H itself;
+ * otherwise it must not overlap H. workspace must hold
+ * sm_moe_block_workspace(...) bytes. */
+int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes);
+int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps, uint64_t Wr, uint64_t bias,
+                 uint64_t arena, uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff,
+                 int experts, int topk, uint64_t Hout, uint64_t ids, uint64_t weights, uint64_t workspace,
+                 uint64_t workspace_bytes);
+
 /* ---------------------------------------------------------------- timing */
 /* Events on the context's stream (the stream every launch above uses). */
 int sm_event_record(sm_ctx *ctx, int slot);          /* slot in [0, 64) */

@@ -66,6 +66,9 @@ def lib():
             "sm_moe_dispatch": (i, [vp, u64, i, i, i, u64, u64, u64, u64, u64, u64]),
             "sm_moe_layer_workspace": (i, [i, i, i, i, i, pu64]),
             "sm_moe_layer": (i, [vp, u64, i, u64, u64, u64, u64, u64, u64, i, i, i, i, u64, u64, u64, u64, u64]),
+            "sm_moe_block_workspace": (i, [i, i, i, i, i, pu64]),
+            "sm_moe_block": (i, [vp, u64, i, u64, ctypes.c_float, u64, u64, u64, u64, u64, u64, i, i, i, i, u64, u64,
+                                 u64, u64, u64]),
             "sm_stage_timing": (i, [vp, i]),
             "sm_stage_report": (i, [vp, ctypes.POINTER(ctypes.c_double), pu64, i]),
             "sm_stage_select": (i, [vp, ctypes.c_uint32]),
@@ -280,6 +283,22 @@ class Backend:
                                        arena.handle, blob_stride, shared_blob.handle, Wsg.handle, width, ff, experts,
                                        topk, Y.handle, ids.handle, weights.handle, workspace.handle,
                                        workspace.nbytes))
+
+    @staticmethod
+    def moe_block_workspace_bytes(tokens, width, ff, experts, topk):
+        n = ctypes.c_uint64()
+        rc = lib().sm_moe_block_workspace(tokens, width, ff, experts, topk, ctypes.byref(n))
+        if rc != SM_OK:
+            raise ArgumentError(rc, "invalid MoE geometry")
+        return n.value
+
+    def moe_block(self, H, tokens, gamma, eps, Wr, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk,
+                  Hout, ids, weights, workspace, bias=None):
+        """Hout = H + MoE(RMSNorm(H; gamma, eps)), one layer of the stack."""
+        self._check(lib().sm_moe_block(self._ctx, H.handle, tokens, gamma.handle, eps, Wr.handle,
+                                       bias.handle if bias else 0, arena.handle, blob_stride, shared_blob.handle,
+                                       Wsg.handle, width, ff, experts, topk, Hout.handle, ids.handle, weights.handle,
+                                       workspace.handle, workspace.nbytes))
 
     # ------------------------------------------------------------ timing
     STAGES = ["decode_route", "decode_gate_up", "decode_down_combine", "prefill_route", "prefill_dispatch",

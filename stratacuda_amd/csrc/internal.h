@@ -96,15 +96,26 @@ int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int exper
 int dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint64_t offsets, uint64_t rows,
              uint64_t parts, uint64_t where_, uint64_t workspace, uint64_t workspace_bytes, int extra_rows);
 uint64_t dispatch_workspace(int tokens, int experts);
+// One block of the 48-layer stack around the MoE stage: the stage's input is
+// RMSNorm(X; gamma, eps) (strata_norm mode 0) and its output is X + y
+// (strata_elementwise mode 5). Null means the plain stage.
+struct BlockArgs {
+    uint64_t gamma;
+    float eps;
+};
 int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
                uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y,
-               uint64_t ids, uint64_t weights, uint64_t workspace, uint64_t workspace_bytes);
+               uint64_t ids, uint64_t weights, uint64_t workspace, uint64_t workspace_bytes,
+               const BlockArgs *block = nullptr);
 uint64_t moe_decode_workspace(int width, int ff, int experts, int topk);
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
                 uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
                 int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,
-                uint64_t workspace_bytes);
-uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk);
+                uint64_t workspace_bytes, const BlockArgs *block = nullptr);
+// With block != nullptr the workspace also holds the normalised input.
+uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk, bool block = false);
+// strata_norm mode 0 (scale 1) over `rows` rows of `cols`, on the context's stream.
+int norm_launch(sm_ctx *ctx, const float *X, const float *gamma, float *Y, int cols, int rows, float eps);
 
 // Byte sizes of the regions of one Q2 expert blob.
 struct BlobLayout {

@@ -604,6 +604,16 @@ const Entry *find_entry(const char *name) {
 
 }  // namespace
 
+namespace smi {
+
+int norm_launch(sm_ctx *ctx, const float *X, const float *gamma, float *Y, int cols, int rows, float eps) {
+    k_norm<<<blocks_for((uint64_t)rows), 256, 0, ctx->stream>>>(X, gamma, Y, cols, rows, 1, 0, eps, 1.0f,
+                                                              (uint64_t)rows);
+    return launched(ctx);
+}
+
+}  // namespace smi
+
 extern "C" {
 
 int sm_kernel_count(void) { return kEntryCount; }

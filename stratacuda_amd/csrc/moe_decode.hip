@@ -157,10 +157,8 @@ __device__ __forceinline__ float dot64_q(uint4 c, const XQ &q) {
 // Quantizes group g of X (one wave, lane i <-> x[64 g + i]) into its record.
 // `bytes` is 192 bytes of this wave's LDS; the caller synchronises the block
 // between the two halves (writes to LDS, then the packed words to memory).
-__device__ __forceinline__ void quantize_group_bytes(const float *__restrict__ X, int g, uint8_t *bytes,
-                                                     float &unit, int &sum) {
+__device__ __forceinline__ void quantize_group_bytes(float x, uint8_t *bytes, float &unit, int &sum) {
     const int lane = threadIdx.x & 63;
-    const float x = X[g * 64 + lane];
     const bool bad = __ballot(!(fabsf(x) <= 3.402823466e38f)) != 0;
     const float m = sm::wave_max(fabsf(x));
     int X_ = 0;
@@ -182,6 +180,24 @@ __device__ __forceinline__ void quantize_group_bytes(const float *__restrict__ X
     bytes[64 + at] = (uint8_t)l1;
     bytes[128 + at] = (uint8_t)l2;
     sum = sm::wave_sum_i32(X_);
+}
+
+// RMSNorm of one row by one wave, exactly as strata_norm mode 0 with scale 1
+// (kernels/strata.cu:214-227): lane-strided sum of squares, the 64-lane
+// tree, inv = 1 / sqrt(ss / cols + eps); element i is then (x_i * inv) * g_i.
+__device__ __forceinline__ float rms_inv_wave(const float *__restrict__ x, int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    float ss = 0.0f;
+    for (int i0 = lane; i0 < cols; i0 += 8 * 64) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = x[min(i0 + 64 * u, cols - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + 64 * u < cols) ss = ss + v[u] * v[u];
+    }
+    ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm::tree_sum64(ss)), 0));
+    return 1.0f / sqrtf(ss / (float)cols + eps);
 }
 
 constexpr int GU_ROWS = 4;  // hidden rows per wave
@@ -232,12 +248,14 @@ __device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, co
 // K1. Blocks [0, route_blocks): 4 router rows each (row `experts` = shared
 // gate), one wave per row in the reference's exact f32 order. Blocks after
 // that: one wave per 64-value group of X writes the group's fixed-point record.
-template <int NJ>
+// NORM: the layer input is RMSNorm(X; gamma, eps) (strata_norm mode 0), which
+// every wave forms itself from X, bit-identical to the separate kernel.
+template <int NJ, bool NORM>
 __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ X, const float *__restrict__ Wr,
                                                       const float *__restrict__ bias, const float *__restrict__ Wsg,
                                                       float *__restrict__ logits, float *__restrict__ gate_out,
                                                       uint32_t *__restrict__ xq, int width, int experts,
-                                                      int route_blocks) {
+                                                      int route_blocks, const float *__restrict__ gamma, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if ((int)blockIdx.x >= route_blocks) {
         __shared__ uint8_t s_bytes[4][192];
@@ -245,7 +263,12 @@ __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ 
         const bool live = g < width / 64;
         float unit = 0.0f;
         int sum = 0;
-        if (live) quantize_group_bytes(X, g, s_bytes[wave], unit, sum);
+        if (live) {
+            const int i = g * 64 + lane;
+            float x = X[i];
+            if (NORM) x = (x * rms_inv_wave(X, width, eps)) * gamma[i];
+            quantize_group_bytes(x, s_bytes[wave], unit, sum);
+        }
         __syncthreads();
         if (live) {
             uint32_t *rec = xq + (uint64_t)g * XQ_WORDS;
@@ -260,15 +283,27 @@ __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ 
     const float *w = row < experts ? Wr + (int64_t)row * width : Wsg;
     float sum = 0.0f;
     if (NJ > 0) {
-        float wv[NJ > 0 ? NJ : 1], xv[NJ > 0 ? NJ : 1];
+        float wv[NJ > 0 ? NJ : 1], xv[NJ > 0 ? NJ : 1], gv[NJ > 0 && NORM ? NJ : 1];
 #pragma unroll
         for (int j = 0; j < NJ; j++) wv[j] = __builtin_nontemporal_load(w + lane + 64 * j);
 #pragma unroll
         for (int j = 0; j < NJ; j++) xv[j] = X[lane + 64 * j];
+        if (NORM) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) gv[j] = gamma[lane + 64 * j];
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) ss = ss + xv[j] * xv[j];
+            ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm::tree_sum64(ss)), 0));
+            const float inv = 1.0f / sqrtf(ss / (float)width + eps);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) xv[j] = (xv[j] * inv) * gv[j];
+        }
 #pragma unroll
         for (int j = 0; j < NJ; j++) sum = sum + wv[j] * xv[j];
     } else {
-        for (int i = lane; i < width; i += 64) sum = sum + w[i] * X[i];
+        const float inv = NORM ? rms_inv_wave(X, width, eps) : 1.0f;
+        for (int i = lane; i < width; i += 64) sum = sum + w[i] * (NORM ? (X[i] * inv) * gamma[i] : X[i]);
     }
     sum = sm::tree_sum64(sum);
     if (lane == 0) {
@@ -316,16 +351,17 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
 
 // K3, the combine at its end shared by both variants (kernels/strata.cu:360-365):
 // y = shared * sigmoid(gate) + sum_k part_k * w_k, in that order.
+// With `resid`, Y = resid + y (strata_elementwise mode 5, scale 1).
 __device__ __forceinline__ void down_combine(const float *parts, const float *__restrict__ weights,
                                              const float *__restrict__ gate, float *__restrict__ Y, int width,
-                                             int topk, const uint64_t *s_tab) {
+                                             int topk, const uint64_t *s_tab, const float *__restrict__ resid) {
     const int tid = threadIdx.x;
     if (tid < 8) {
         const int row = blockIdx.x * 8 + tid;
         if (row < width) {
             float value = parts[topk * 8 + tid] * sm::sigmoid(gate[0], s_tab);
             for (int k = 0; k < topk; k++) value = value + parts[k * 8 + tid] * weights[k];
-            Y[row] = value;
+            Y[row] = resid ? resid[row] + value : value;
         }
     }
 }
@@ -351,7 +387,8 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
                                                               const float *__restrict__ weights,
                                                               const float *__restrict__ gate, float *__restrict__ Y,
                                                               int width, int ff, int topk, int experts,
-                                                              uint64_t down_codes, uint64_t down_scales) {
+                                                              uint64_t down_codes, uint64_t down_scales,
+                                                              const float *__restrict__ resid) {
     static_assert(NQ >= 1 && NQ <= DN_MAX_SLOTS, "slots per wave");
     __shared__ float parts[33 * 8];
     __shared__ uint64_t s_tab[32];
@@ -426,7 +463,7 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
         if (gl == 0 && k < nexp) parts[k * 8 + rr] = v;
     }
     __syncthreads();
-    down_combine(parts, weights, gate, Y, width, topk, s_tab);
+    down_combine(parts, weights, gate, Y, width, topk, s_tab, resid);
 }
 
 // K3 for any other shape: hidden groups read from memory, lanes loop over
@@ -437,7 +474,7 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
                                                           const int *__restrict__ ids, const float *__restrict__ weights,
                                                           const float *__restrict__ gate, float *__restrict__ Y,
                                                           int width, int ff, int topk, int experts, uint64_t down_codes,
-                                                          uint64_t down_scales) {
+                                                          uint64_t down_scales, const float *__restrict__ resid) {
     __shared__ float parts[33 * 8];
     __shared__ uint64_t s_tab[32];
     const int nexp = topk + 1, GF = ff / 64;
@@ -461,7 +498,7 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
         if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
     }
     __syncthreads();
-    down_combine(parts, weights, gate, Y, width, topk, s_tab);
+    down_combine(parts, weights, gate, Y, width, topk, s_tab, resid);
 }
 
 constexpr uint64_t kAlign = 256;
@@ -488,7 +525,10 @@ uint64_t moe_decode_workspace(int width, int ff, int experts, int topk) { return
 
 int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
                uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y, uint64_t ids,
-               uint64_t weights, uint64_t workspace, uint64_t workspace_bytes) {
+               uint64_t weights, uint64_t workspace, uint64_t workspace_bytes, const BlockArgs *block) {
+    const float *gamma = block ? (const float *)block->gamma : nullptr;
+    const float eps = block ? block->eps : 0.0f;
+    const float *resid = block ? (const float *)X : nullptr;
     (void)workspace_bytes;
     DecodeWs w = decode_ws(width, ff, experts, topk);
     char *ws = (char *)workspace;
@@ -501,14 +541,13 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
         if (int rc = stage_mark(ctx, kStageDecodeRoute)) return rc;
         const int route_blocks = ceil_div(experts + 1, 4);
         const unsigned grid = (unsigned)(route_blocks + ceil_div(width / 64, 4));
-        if (width == 2048)
-            k_decode_route<32><<<grid, 256, 0, ctx->stream>>>(
-                (const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg, (float *)(ws + w.logits),
-                (float *)(ws + w.gate), xq, width, experts, route_blocks);
-        else
-            k_decode_route<0><<<grid, 256, 0, ctx->stream>>>(
-                (const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg, (float *)(ws + w.logits),
-                (float *)(ws + w.gate), xq, width, experts, route_blocks);
+        using K1 = void (*)(const float *, const float *, const float *, const float *, float *, float *, uint32_t *,
+                            int, int, int, const float *, float);
+        const K1 k1 = width == 2048 ? (gamma ? k_decode_route<32, true> : k_decode_route<32, false>)
+                                    : (gamma ? k_decode_route<0, true> : k_decode_route<0, false>);
+        k1<<<grid, 256, 0, ctx->stream>>>((const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg,
+                                          (float *)(ws + w.logits), (float *)(ws + w.gate), xq, width, experts,
+                                          route_blocks, gamma, eps);
         if (int rc = launched(ctx)) return rc;
     }
     // 2. top-k (per routed block) + gate/up of the routed and shared experts
@@ -524,7 +563,7 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
     if (stage_on(ctx, kStageDecodeDown)) {
         if (int rc = stage_mark(ctx, kStageDecodeDown)) return rc;
         using K3 = void (*)(const float *, const uint8_t *, uint64_t, const uint8_t *, const int *, const float *,
-                            const float *, float *, int, int, int, int, uint64_t, uint64_t);
+                            const float *, float *, int, int, int, int, uint64_t, uint64_t, const float *);
         static const K3 by_slots[DN_MAX_SLOTS] = {k_decode_down<1>, k_decode_down<2>, k_decode_down<3>,
                                                   k_decode_down<4>, k_decode_down<5>};
         const bool narrow = ff <= 512;
@@ -532,7 +571,7 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
         kernel<<<(unsigned)ceil_div(width, 8), narrow ? 64 * DN_WAVES : 256, 0, ctx->stream>>>(
             hidden, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const int *)ids,
             (const float *)weights, (const float *)(ws + w.gate), (float *)Y, width, ff, topk, experts, L.down_codes,
-            L.down_scales);
+            L.down_scales, resid);
         if (int rc = launched(ctx)) return rc;
     }
     return stage_mark(ctx, -1);

@@ -685,7 +685,8 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
 }
 
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
-// in the reference order (kernels/strata.cu:470-476). One block per token:
+// in the reference order (kernels/strata.cu:470-476); with `resid`,
+// Y = resid + that (strata_elementwise mode 5). One block per token:
 // the token's slot positions, weights and sigmoid(gate) are read once, then
 // each thread combines 4 consecutive outputs per step with 16-byte loads.
 // Needs width % 4 == 0.
@@ -693,7 +694,7 @@ constexpr int COMBINE_MAX_K = 32;
 __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, const int *__restrict__ where_,
                                                  const float *__restrict__ weights, const float *__restrict__ gate,
                                                  const int *__restrict__ offsets, float *__restrict__ Y, int tokens,
-                                                 int topk, int width, int experts) {
+                                                 int topk, int width, int experts, const float *__restrict__ resid) {
     __shared__ int s_pos[COMBINE_MAX_K];
     __shared__ float s_w[COMBINE_MAX_K];
     __shared__ float s_sig;
@@ -719,6 +720,10 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, co
             v.z = v.z + part.z * w;
             v.w = v.w + part.w * w;
         }
+        if (resid) {
+            const float4 h = ((const float4 *)(resid + (int64_t)t * width))[d4];
+            v = make_float4(h.x + v.x, h.y + v.y, h.z + v.z, h.w + v.w);
+        }
         ((float4 *)(Y + (int64_t)t * width))[d4] = v;
     }
 }
@@ -736,9 +741,9 @@ inline uint64_t big_tile_bound(uint64_t m, int experts) {
 
 struct PrefillWs {
     uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, rows, parts, where_, Xhl,
-        Hhl, P, end;
+        Hhl, P, Xn, end;
 };
-PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
+PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool block = false) {
     const uint64_t n = (uint64_t)tokens * topk, m = n + tokens;
     PrefillWs w;
     w.logits = 0;
@@ -755,7 +760,8 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
     w.Xhl = up(w.where_ + n * 4);
     w.Hhl = up(w.Xhl + (uint64_t)tokens * width * 4);
     w.P = up(w.Hhl + m * ff * 4);
-    w.end = up(w.P + m * width * 4);
+    w.Xn = up(w.P + m * width * 4);
+    w.end = block ? up(w.Xn + (uint64_t)tokens * width * 4) : w.Xn;
     return w;
 }
 
@@ -763,16 +769,25 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk) {
 
 namespace smi {
 
-uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk) {
-    return prefill_ws(tokens, width, ff, experts, topk).end;
+uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk, bool block) {
+    return prefill_ws(tokens, width, ff, experts, topk, block).end;
 }
 
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
                 uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y, uint64_t ids,
-                uint64_t weights, uint64_t workspace, uint64_t workspace_bytes) {
+                uint64_t weights, uint64_t workspace, uint64_t workspace_bytes, const BlockArgs *block) {
     (void)workspace_bytes;
-    PrefillWs w = prefill_ws(tokens, width, ff, experts, topk);
+    PrefillWs w = prefill_ws(tokens, width, ff, experts, topk, block != nullptr);
     char *ws = (char *)workspace;
+    const float *resid = nullptr;
+    if (block) {
+        // The stage runs on RMSNorm(X) and the combine adds X back.
+        if (int rc = norm_launch(ctx, (const float *)X, (const float *)block->gamma, (float *)(ws + w.Xn), width,
+                                 tokens, block->eps))
+            return rc;
+        resid = (const float *)X;
+        X = (uint64_t)(ws + w.Xn);
+    }
     BlobLayout L = blob_layout(width, ff);
     if ((2 * ff) % 128 || width % 128)
         return fail(ctx, SM_E_ARG, "prefill needs width and 2*ff to be multiples of 128");
@@ -868,7 +883,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     (void)total;
     k_combine<<<(unsigned)tokens, 256, 0, ctx->stream>>>(
         (const float *)(ws + w.P), (const int *)(ws + w.where_), (const float *)weights, (const float *)(ws + w.gate),
-        offsets, (float *)Y, tokens, topk, width, experts);
+        offsets, (float *)Y, tokens, topk, width, experts, resid);
     if (int rc = launched(ctx)) return rc;
     return stage_mark(ctx, -1);
 }

@@ -358,6 +358,47 @@ int sm_moe_dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts
     return dispatch(ctx, ids, tokens, topk, experts, offsets, rows, parts, where_, workspace, workspace_bytes, 0);
 }
 
+int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps, uint64_t Wr, uint64_t bias,
+                 uint64_t arena, uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff,
+                 int experts, int topk, uint64_t Hout, uint64_t ids, uint64_t weights, uint64_t workspace,
+                 uint64_t workspace_bytes) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = check_geometry(ctx, tokens, width, ff, experts, topk)) return rc;
+    if (!(eps >= 0.0f)) return fail(ctx, SM_E_ARG, "epsilon must be >= 0");
+    BlobLayout L = blob_layout(width, ff);
+    if (blob_stride < L.bytes || blob_stride % 256)
+        return fail(ctx, SM_E_ARG, "blob stride must be a multiple of 256 holding one blob");
+    if (int rc = need(ctx, arena, blob_stride * (uint64_t)(experts - 1) + L.bytes, "expert arena")) return rc;
+    if (int rc = need(ctx, shared_blob, L.bytes, "shared expert blob")) return rc;
+    if (int rc = need(ctx, H, (uint64_t)tokens * width * 4, "H")) return rc;
+    if (int rc = need(ctx, Hout, (uint64_t)tokens * width * 4, "Hout")) return rc;
+    if (int rc = need(ctx, gamma, (uint64_t)width * 4, "gamma")) return rc;
+    if (int rc = need(ctx, Wr, (uint64_t)experts * width * 4, "router weights")) return rc;
+    if (int rc = need(ctx, Wsg, (uint64_t)width * 4, "shared gate weights")) return rc;
+    if (bias)
+        if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
+    if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
+    if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
+    uint64_t ws = tokens == 1 ? moe_decode_workspace(width, ff, experts, topk)
+                              : moe_prefill_workspace(tokens, width, ff, experts, topk, true);
+    if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
+    if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
+    if (Hout != H && Hout < H + (uint64_t)tokens * width * 4 && H < Hout + (uint64_t)tokens * width * 4)
+        return fail(ctx, SM_E_ARG, "Hout must be H itself or not overlap it");
+    const BlockArgs block = {gamma, eps};
+    if (tokens == 1)
+        return moe_decode(ctx, H, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout, ids,
+                          weights, workspace, workspace_bytes, &block);
+    return moe_prefill(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout,
+                       ids, weights, workspace, workspace_bytes, &block);
+}
+
+int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes) {
+    if (int rc = sm_moe_layer_workspace(tokens, width, ff, experts, topk, bytes)) return rc;
+    if (tokens > 1) *bytes = moe_prefill_workspace(tokens, width, ff, experts, topk, true);
+    return SM_OK;
+}
+
 int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes) {
     if (!bytes || tokens < 1 || width < 64 || ff < 64 || width % 64 || ff % 64 || experts < 1 || experts > 512 ||
         topk < 1 || topk > 32 || topk > experts)

@@ -125,10 +125,13 @@ class DeviceStack:
     ``trace`` keeps every layer's input and routing for checking."""
 
     def __init__(self, backend, layers=48, tokens=1, width=WIDTH, ff=FF, experts=EXPERTS, topk=TOPK,
-                 base_seed=BASE_SEED, trace=False):
+                 base_seed=BASE_SEED, trace=False, fused=True):
         """``layers``: a count, or a list of existing DeviceLayer objects
-        (layer l of the list is layer l of the stack; not freed here)."""
-        self.b, self.T = backend, tokens
+        (layer l of the list is layer l of the stack; not freed here).
+        ``fused``: one sm_moe_block call per layer (normalisation and
+        residual folded into the stage's kernels) instead of the three
+        separate steps; the results are the same bits."""
+        self.b, self.T, self.fused = backend, tokens, fused
         self.width, self.ff, self.experts, self.topk = width, ff, experts, topk
         self.own_layers = not isinstance(layers, list)
         self.layers = ([DeviceLayer(backend, l, width, ff, experts, base_seed) for l in range(layers)]
@@ -139,7 +142,7 @@ class DeviceStack:
         self.Xn, self.Y = backend.alloc(n, zero=False), backend.alloc(n, zero=False)
         self.ids = [backend.alloc(tokens * topk, "i32") for _ in range(layers if trace else 1)]
         self.w = [backend.alloc(tokens * topk) for _ in range(layers if trace else 1)]
-        self.ws = backend.alloc_bytes(backend.moe_workspace_bytes(tokens, width, ff, experts, topk))
+        self.ws = backend.alloc_bytes(backend.moe_block_workspace_bytes(tokens, width, ff, experts, topk))
         self.trace = trace
 
     def input(self, seed):
@@ -154,6 +157,10 @@ class DeviceStack:
             h_in = self.H[l if self.trace else l % 2]
             h_out = self.H[l + 1 if self.trace else (l + 1) % 2]
             ids, w = self.ids[l if self.trace else 0], self.w[l if self.trace else 0]
+            if self.fused:
+                b.moe_block(h_in, T, lay.gamma, 1e-6, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, self.ff,
+                            self.experts, self.topk, h_out, ids, w, self.ws)
+                continue
             b.run("strata_norm", {"X": h_in, "W": lay.gamma, "Y": self.Xn, "cols": W, "rows": T, "weightRows": 1,
                                   "mode": 0, "epsilon": 1e-6, "scale": 1.0}, [T, 1, 1])
             b.moe_layer(self.Xn, T, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, self.ff, self.experts,

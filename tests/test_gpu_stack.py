@@ -77,3 +77,29 @@ def test_stack_batch32(backend, oracle, stack_layers):
             check_layer(backend, oracle, st, l, [0, 13, 31])
     finally:
         st.free()
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_block_entry_matches_separate_steps(backend, stack_layers, tokens):
+    """sm_moe_block (normalisation and residual folded into the stage) gives
+    the same bits as strata_norm, sm_moe_layer and strata_elementwise run
+    one after the other, over four layers, also when writing in place."""
+    fused = wl.DeviceStack(backend, layers=stack_layers[:4], tokens=tokens, trace=True, fused=True)
+    split = wl.DeviceStack(backend, layers=stack_layers[:4], tokens=tokens, trace=True, fused=False)
+    try:
+        for st in (fused, split):
+            st.input(wl.BASE_SEED + 77 + tokens)
+            st.step()
+        for l in range(1, 5):
+            assert same_bits(backend.read(fused.H[l]), backend.read(split.H[l])), "layer %d" % (l - 1)
+            assert np.array_equal(backend.read(fused.ids[l - 1]), backend.read(split.ids[l - 1]))
+        # in place: H <- H + MoE(RMSNorm(H))
+        lay = stack_layers[0]
+        W = wl.WIDTH
+        backend.copy(split.H[0], fused.H[1], tokens * W)
+        backend.moe_block(fused.H[1], tokens, lay.gamma, 1e-6, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg,
+                          W, wl.FF, wl.EXPERTS, wl.TOPK, fused.H[1], fused.ids[0], fused.w[0], fused.ws)
+        assert same_bits(backend.read(fused.H[1]), backend.read(split.H[1]))
+    finally:
+        fused.free()
+        split.free()
