@@ -117,8 +117,9 @@ int sm_moe_dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts
  * ff/4 B), gate/up fp16 scales, down fp16 scales; 64-weight groups; weight =
  * (code - 1) * scale. width and ff must be multiples of 64.
  * ids/weights (tokens x topk) receive the routing. workspace must hold
- * sm_moe_layer_workspace(...) bytes. tokens == 1 runs the decode kernels
- * (GEMV); tokens > 1 runs dispatch + grouped MFMA GEMMs. */
+ * sm_moe_layer_workspace(...) bytes. Up to 16 tokens run the decode kernels
+ * (GEMV, one grid slice per token); more tokens run dispatch + grouped MFMA
+ * GEMMs. */
 int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes);
 int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
                  uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
@@ -131,9 +132,9 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
  * sm_moe_layer, and strata_elementwise mode 5, :230-236):
  *   Hout = H + MoE(RMSNorm(H; gamma, eps))          per token.
  * gamma is [width] f32. Results are bit-identical to running those three
- * steps separately. tokens == 1 folds the normalisation into the router
- * kernel and the residual into the down kernel; tokens > 1 normalises into
- * the workspace and adds the residual in the combine. Hout may be H itself;
+ * steps separately. Up to 16 tokens fold the normalisation into the router
+ * kernel and the residual into the down kernel; more tokens normalise into
+ * the workspace and add the residual in the combine. Hout may be H itself;
  * otherwise it must not overlap H. workspace must hold
  * sm_moe_block_workspace(...) bytes. */
 int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes);

@@ -103,11 +103,17 @@ struct BlockArgs {
     uint64_t gamma;
     float eps;
 };
-int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
+// Batches of up to kDecodeMaxTokens tokens run the decode (GEMV) kernels with
+// a token dimension; larger ones the dispatch + grouped GEMM path.
+constexpr int kDecodeMaxTokens = 16;
+constexpr int kDecodeBlockRouting = 4;  // up to this many tokens the gate/up blocks route
+// Exact per-token top-k (strata_router order) of logits [tokens x experts].
+int topk_launch(sm_ctx *ctx, const float *logits, int *ids, float *weights, int tokens, int experts, int topk);
+int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
                uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y,
                uint64_t ids, uint64_t weights, uint64_t workspace, uint64_t workspace_bytes,
                const BlockArgs *block = nullptr);
-uint64_t moe_decode_workspace(int width, int ff, int experts, int topk);
+uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int topk);
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
                 uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
                 int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,

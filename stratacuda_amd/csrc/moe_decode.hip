@@ -257,9 +257,16 @@ __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ 
                                                       uint32_t *__restrict__ xq, int width, int experts,
                                                       int route_blocks, const float *__restrict__ gamma, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    {  // token blockIdx.y
+        const int t = blockIdx.y;
+        X += (int64_t)t * width;
+        logits += (int64_t)t * experts;
+        gate_out += t;
+        xq += (uint64_t)t * (width / 64) * XQ_WORDS;
+    }
     if ((int)blockIdx.x >= route_blocks) {
         __shared__ uint8_t s_bytes[4][192];
-        const int g = ((int)blockIdx.x - route_blocks) * 4 + wave;
+        const int g = ((int)blockIdx.x - route_blocks) * 4 + wave;  // past the groups: padding blocks
         const bool live = g < width / 64;
         float unit = 0.0f;
         int sum = 0;
@@ -321,19 +328,33 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
                                                         const uint8_t *__restrict__ shared_blob,
                                                         const float *__restrict__ logits, int *__restrict__ ids,
                                                         float *__restrict__ weights, float *__restrict__ hidden,
-                                                        int width, int ff, int topk, int experts, uint64_t gu_scales) {
+                                                        int width, int ff, int topk, int experts, uint64_t gu_scales,
+                                                        int routed) {
     __shared__ int s_ids[32];
     __shared__ float s_w[32];
     __shared__ uint64_t s_tab[32];
     __shared__ sm::RouterScratch s_router;
     const int wave = threadIdx.x >> 6, gl = threadIdx.x & 31;
     const int k = blockIdx.y;
+    {  // token blockIdx.z
+        const int t = blockIdx.z;
+        xq += (uint64_t)t * (width / 64) * XQ_WORDS;
+        logits += (int64_t)t * experts;
+        ids += (int64_t)t * topk;
+        weights += (int64_t)t * topk;
+        hidden += (uint64_t)t * (topk + 1) * ff;
+    }
+    // routed: the IDs are already in memory (a top-k kernel ran per token)
+    // and the block reads its slot's ID instead of selecting it itself.
     float l0 = 0.0f, l1 = 0.0f;
-    if (k < topk) sm::router_load(logits, experts, l0, l1);
+    if (k < topk && !routed) sm::router_load(logits, experts, l0, l1);
     XQ first;
     if (gl < width / 64) load_xq(xq, gl, first);
     sm::fill_exp_table(s_tab);
-    if (k < topk) {
+    if (k < topk && routed) {
+        if (threadIdx.x == 0) s_ids[k] = ids[k];
+        __syncthreads();
+    } else if (k < topk) {
         sm::router_block(l0, l1, experts, topk, s_tab, s_router, s_ids, s_w);
         __syncthreads();
         if (blockIdx.x == 0 && k == 0 && (int)threadIdx.x < topk) {
@@ -390,6 +411,15 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
                                                               uint64_t down_codes, uint64_t down_scales,
                                                               const float *__restrict__ resid) {
     static_assert(NQ >= 1 && NQ <= DN_MAX_SLOTS, "slots per wave");
+    {  // token blockIdx.y
+        const int t = blockIdx.y;
+        hidden += (uint64_t)t * (topk + 1) * ff;
+        ids += (int64_t)t * topk;
+        weights += (int64_t)t * topk;
+        gate += t;
+        Y += (int64_t)t * width;
+        if (resid) resid += (int64_t)t * width;
+    }
     __shared__ float parts[33 * 8];
     __shared__ uint64_t s_tab[32];
     __shared__ __attribute__((aligned(16))) float s_h[DN_WAVES][8 * DN_PITCH];
@@ -475,6 +505,15 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
                                                           const float *__restrict__ gate, float *__restrict__ Y,
                                                           int width, int ff, int topk, int experts, uint64_t down_codes,
                                                           uint64_t down_scales, const float *__restrict__ resid) {
+    {  // token blockIdx.y
+        const int t = blockIdx.y;
+        hidden += (uint64_t)t * (topk + 1) * ff;
+        ids += (int64_t)t * topk;
+        weights += (int64_t)t * topk;
+        gate += t;
+        Y += (int64_t)t * width;
+        if (resid) resid += (int64_t)t * width;
+    }
     __shared__ float parts[33 * 8];
     __shared__ uint64_t s_tab[32];
     const int nexp = topk + 1, GF = ff / 64;
@@ -507,13 +546,14 @@ inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 struct DecodeWs {
     uint64_t logits, gate, xq, hidden, end;
 };
-DecodeWs decode_ws(int width, int ff, int experts, int topk) {
+DecodeWs decode_ws(int tokens, int width, int ff, int experts, int topk) {
+    const uint64_t T = (uint64_t)tokens;
     DecodeWs w;
     w.logits = 0;
-    w.gate = up(w.logits + (uint64_t)experts * 4);
-    w.xq = up(w.gate + 4);
-    w.hidden = up(w.xq + (uint64_t)(width / 64) * XQ_WORDS * 4);
-    w.end = up(w.hidden + (uint64_t)(topk + 1) * ff * 4);
+    w.gate = up(w.logits + T * experts * 4);
+    w.xq = up(w.gate + T * 4);
+    w.hidden = up(w.xq + T * (width / 64) * XQ_WORDS * 4);
+    w.end = up(w.hidden + T * (topk + 1) * ff * 4);
     return w;
 }
 
@@ -521,16 +561,18 @@ DecodeWs decode_ws(int width, int ff, int experts, int topk) {
 
 namespace smi {
 
-uint64_t moe_decode_workspace(int width, int ff, int experts, int topk) { return decode_ws(width, ff, experts, topk).end; }
+uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int topk) {
+    return decode_ws(tokens, width, ff, experts, topk).end;
+}
 
-int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
+int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
                uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts, int topk, uint64_t Y, uint64_t ids,
                uint64_t weights, uint64_t workspace, uint64_t workspace_bytes, const BlockArgs *block) {
     const float *gamma = block ? (const float *)block->gamma : nullptr;
     const float eps = block ? block->eps : 0.0f;
     const float *resid = block ? (const float *)X : nullptr;
     (void)workspace_bytes;
-    DecodeWs w = decode_ws(width, ff, experts, topk);
+    DecodeWs w = decode_ws(tokens, width, ff, experts, topk);
     char *ws = (char *)workspace;
     BlobLayout L = blob_layout(width, ff);
     float *hidden = (float *)(ws + w.hidden);
@@ -539,8 +581,10 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
     // 1. router logits + shared gate logit + fixed-point activations
     if (stage_on(ctx, kStageDecodeRoute)) {
         if (int rc = stage_mark(ctx, kStageDecodeRoute)) return rc;
+        // grid.x a multiple of 8: block (x, t) runs on XCD x % 8 for every
+        // token t, so each XCD reads its share of W_r from memory once.
         const int route_blocks = ceil_div(experts + 1, 4);
-        const unsigned grid = (unsigned)(route_blocks + ceil_div(width / 64, 4));
+        const dim3 grid((unsigned)((route_blocks + ceil_div(width / 64, 4) + 7) / 8 * 8), (unsigned)tokens);
         using K1 = void (*)(const float *, const float *, const float *, const float *, float *, float *, uint32_t *,
                             int, int, int, const float *, float);
         const K1 k1 = width == 2048 ? (gamma ? k_decode_route<32, true> : k_decode_route<32, false>)
@@ -550,13 +594,21 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
                                           route_blocks, gamma, eps);
         if (int rc = launched(ctx)) return rc;
     }
-    // 2. top-k (per routed block) + gate/up of the routed and shared experts
+    // 2. top-k + gate/up of the routed and shared experts. Up to
+    // kDecodeBlockRouting tokens every routed block selects its token's
+    // experts itself (no extra launch); beyond that the per-block selections
+    // would cost more than one top-k kernel per token.
+    const int routed = tokens > kDecodeBlockRouting ? 1 : 0;
+    if (routed && stage_on(ctx, kStageDecodeGateUp))
+        if (int rc = topk_launch(ctx, (const float *)(ws + w.logits), (int *)ids, (float *)weights, tokens, experts,
+                                 topk))
+            return rc;
     if (stage_on(ctx, kStageDecodeGateUp)) {
         if (int rc = stage_mark(ctx, kStageDecodeGateUp)) return rc;
-        dim3 g1((unsigned)blocks_per_expert, (unsigned)(topk + 1));
+        dim3 g1((unsigned)blocks_per_expert, (unsigned)(topk + 1), (unsigned)tokens);
         k_decode_gate_up<<<g1, 64 * GU_WAVES, 0, ctx->stream>>>(
             xq, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const float *)(ws + w.logits),
-            (int *)ids, (float *)weights, hidden, width, ff, topk, experts, L.gate_up_scales);
+            (int *)ids, (float *)weights, hidden, width, ff, topk, experts, L.gate_up_scales, routed);
         if (int rc = launched(ctx)) return rc;
     }
     // 3. down for all experts + combine
@@ -568,7 +620,7 @@ int moe_decode(sm_ctx *ctx, uint64_t X, uint64_t Wr, uint64_t bias, uint64_t are
                                                   k_decode_down<4>, k_decode_down<5>};
         const bool narrow = ff <= 512;
         const K3 kernel = narrow ? by_slots[ceil_div(topk + 1, DN_WAVES) - 1] : k_decode_down_wide;
-        kernel<<<(unsigned)ceil_div(width, 8), narrow ? 64 * DN_WAVES : 256, 0, ctx->stream>>>(
+        kernel<<<dim3((unsigned)ceil_div(width, 8), (unsigned)tokens), narrow ? 64 * DN_WAVES : 256, 0, ctx->stream>>>(
             hidden, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const int *)ids,
             (const float *)weights, (const float *)(ws + w.gate), (float *)Y, width, ff, topk, experts, L.down_codes,
             L.down_scales, resid);

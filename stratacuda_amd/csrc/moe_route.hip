@@ -354,6 +354,11 @@ namespace smi {
 
 uint64_t dispatch_workspace(int tokens, int experts) { return dispatch_ws(tokens, experts).end; }
 
+int topk_launch(sm_ctx *ctx, const float *logits, int *ids, float *weights, int tokens, int experts, int topk) {
+    k_topk<<<ceil_div(tokens, 4), 256, 0, ctx->stream>>>(logits, ids, weights, tokens, experts, topk);
+    return launched(ctx);
+}
+
 int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float *Wr, const float *bias, int experts,
                  int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out) {
     if (tokens == 1) {

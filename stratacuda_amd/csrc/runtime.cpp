@@ -379,15 +379,15 @@ int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps,
         if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
     if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
     if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
-    uint64_t ws = tokens == 1 ? moe_decode_workspace(width, ff, experts, topk)
+    uint64_t ws = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                               : moe_prefill_workspace(tokens, width, ff, experts, topk, true);
     if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
     if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
     if (Hout != H && Hout < H + (uint64_t)tokens * width * 4 && H < Hout + (uint64_t)tokens * width * 4)
         return fail(ctx, SM_E_ARG, "Hout must be H itself or not overlap it");
     const BlockArgs block = {gamma, eps};
-    if (tokens == 1)
-        return moe_decode(ctx, H, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout, ids,
+    if (tokens <= kDecodeMaxTokens)
+        return moe_decode(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout, ids,
                           weights, workspace, workspace_bytes, &block);
     return moe_prefill(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout,
                        ids, weights, workspace, workspace_bytes, &block);
@@ -395,7 +395,7 @@ int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps,
 
 int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes) {
     if (int rc = sm_moe_layer_workspace(tokens, width, ff, experts, topk, bytes)) return rc;
-    if (tokens > 1) *bytes = moe_prefill_workspace(tokens, width, ff, experts, topk, true);
+    if (tokens > kDecodeMaxTokens) *bytes = moe_prefill_workspace(tokens, width, ff, experts, topk, true);
     return SM_OK;
 }
 
@@ -403,7 +403,7 @@ int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk,
     if (!bytes || tokens < 1 || width < 64 || ff < 64 || width % 64 || ff % 64 || experts < 1 || experts > 512 ||
         topk < 1 || topk > 32 || topk > experts)
         return SM_E_ARG;
-    *bytes = tokens == 1 ? moe_decode_workspace(width, ff, experts, topk)
+    *bytes = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                          : moe_prefill_workspace(tokens, width, ff, experts, topk);
     return SM_OK;
 }
@@ -426,12 +426,12 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
         if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
     if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
     if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
-    uint64_t ws = tokens == 1 ? moe_decode_workspace(width, ff, experts, topk)
+    uint64_t ws = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                               : moe_prefill_workspace(tokens, width, ff, experts, topk);
     if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
     if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
-    if (tokens == 1)
-        return moe_decode(ctx, X, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
+    if (tokens <= kDecodeMaxTokens)
+        return moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
                           weights, workspace, workspace_bytes);
     return moe_prefill(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
                        weights, workspace, workspace_bytes);
