@@ -32,16 +32,22 @@ using namespace smi;
 
 namespace {
 
-// ------------------------------------------------------------ T = 1 route
-// One 64-thread block per row: rows [0, experts) are router rows, row
-// `experts` is the shared-expert gate (when gate_w != 0). NJ = width / 64
-// loads per lane, all issued before the (sequential, reference-order) sum.
+// ---------------------------------------------------- route, few tokens
+// One 64-thread block per (row, token): rows [0, experts) are router rows,
+// row `experts` is the shared-expert gate (when gate_w != 0); blocks past the
+// last row (grid.x is padded to a multiple of 8, so a row's blocks run on one
+// XCD for every token) return. NJ = width / 64 loads per lane, all issued
+// before the (sequential, reference-order) sum.
 template <int NJ>
 __global__ void __launch_bounds__(64) k_route_rows(const float *__restrict__ X, const float *__restrict__ Wr,
                                                    const float *__restrict__ bias, const float *__restrict__ Wsg,
                                                    float *__restrict__ logits, float *__restrict__ gate_out, int width,
-                                                   int experts) {
-    const int row = blockIdx.x, lane = threadIdx.x;
+                                                   int experts, int rows) {
+    const int row = blockIdx.x, lane = threadIdx.x, t = blockIdx.y;
+    if (row >= rows) return;
+    X += (int64_t)t * width;
+    logits += (int64_t)t * experts;
+    gate_out += t;
     const float *w = row < experts ? Wr + (int64_t)row * width : Wsg;
     float sum = 0.0f;
     if (NJ > 0) {
@@ -301,6 +307,84 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_scan(const int *__res
     }
 }
 
+// The whole dispatch for up to 64 tokens (one token block) in one block of
+// SCAN_THREADS threads: masks in LDS, expert offsets by a block scan, tilings
+// and tile records, then the placement (same results as masks + scan + place).
+__global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_one(const int *__restrict__ ids, int tokens, int topk,
+                                                               int experts, int *__restrict__ offsets,
+                                                               int *__restrict__ rows, int *__restrict__ parts,
+                                                               int *__restrict__ where_, int extra,
+                                                               int *__restrict__ tile_small,
+                                                               int *__restrict__ tile_big, int split, int mt_small,
+                                                               int mt_big, uint32_t *__restrict__ status,
+                                                               int4 *__restrict__ info_small,
+                                                               int4 *__restrict__ info_big) {
+    __shared__ unsigned long long m[512];
+    __shared__ int s_off[513];
+    __shared__ int s_wave[SCAN_THREADS / 64];
+    __shared__ uint32_t s_flags;
+    const int tid = threadIdx.x, n = tokens * topk;
+    for (int e = tid; e < experts; e += SCAN_THREADS) m[e] = 0ull;
+    if (tid == 0) s_flags = 0;
+    __syncthreads();
+    for (int a = tid; a < n; a += SCAN_THREADS) {
+        const int e = ids[a];
+        if (e < 0 || e >= experts) {
+            atomicOr(&s_flags, 1u);
+            continue;
+        }
+        const unsigned long long bit = 1ull << (a / topk);
+        if (atomicOr(&m[e], bit) & bit) atomicOr(&s_flags, 2u);
+    }
+    __syncthreads();
+    const int e = tid;
+    const int tot = e < experts ? __popcll(m[e]) : 0;
+    const int incl = block_inclusive_scan(tot, s_wave), excl = incl - tot;
+    if (e < experts) {
+        offsets[e] = excl;
+        s_off[e] = excl;
+        if (e == experts - 1) {
+            offsets[experts] = incl;
+            offsets[experts + 1] = incl + extra;
+            s_off[experts] = incl;
+        }
+    }
+    const int cnt = e < experts ? tot : e == experts ? extra : 0;
+    int ns = 0, nbg = 0;
+    if (cnt >= split) nbg = (cnt + mt_big - 1) / mt_big;
+    else ns = (cnt + mt_small - 1) / mt_small;
+    const int ts = block_inclusive_scan(ns, s_wave), tb = block_inclusive_scan(nbg, s_wave);
+    if (e == 0) *status = s_flags;  // block scans above synchronised the block
+    if (e <= experts) {
+        tile_small[e + 1] = ts;
+        tile_big[e + 1] = tb;
+        if (e == 0) tile_small[0] = tile_big[0] = 0;
+        int4 *info = ns ? info_small : info_big;
+        const int cnt_t = ns ? ns : nbg, mt = ns ? mt_small : mt_big, first = (ns ? ts : tb) - cnt_t;
+        if (info)
+            for (int j = 0; j < cnt_t; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, 0);
+    }
+    __syncthreads();  // s_off complete
+    for (int a = tid; a < n + (extra ? tokens : 0); a += SCAN_THREADS) {
+        if (a < n) {
+            const int t = a / topk, ex = ids[a];
+            if (ex < 0 || ex >= experts) {
+                where_[a] = -1;
+                continue;
+            }
+            const unsigned long long below = t ? (m[ex] & ((1ull << t) - 1ull)) : 0ull;
+            const int pos = s_off[ex] + __popcll(below);
+            rows[pos] = t;
+            parts[pos] = a;
+            where_[a] = pos;
+        } else {
+            const int t = a - n, at = s_off[experts] + t;
+            rows[at] = t;
+            parts[at] = -1;
+        }
+    }
+}
+
 __global__ void k_dispatch_place(const int *__restrict__ ids, int tokens, int topk, int experts, int nb,
                                  const unsigned long long *__restrict__ masks, const int *__restrict__ base,
                                  int *__restrict__ rows, int *__restrict__ parts, int *__restrict__ where_,
@@ -361,14 +445,19 @@ int topk_launch(sm_ctx *ctx, const float *logits, int *ids, float *weights, int 
 
 int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float *Wr, const float *bias, int experts,
                  int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out) {
-    if (tokens == 1) {
+    if (tokens <= kRouteRowsMaxTokens) {
+        // Few tokens: one wave per (row, token), latency-bound anyway.
         const int total = experts + (gate_w ? 1 : 0);
+        const dim3 grid((unsigned)((total + 7) / 8 * 8), (unsigned)tokens);
         if (width == 2048)
-            k_route_rows<32><<<total, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts);
+            k_route_rows<32><<<grid, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts,
+                                                          total);
         else
-            k_route_rows<0><<<total, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts);
+            k_route_rows<0><<<grid, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts,
+                                                         total);
         if (int rc = launched(ctx)) return rc;
-        k_topk<<<1, 64, 0, ctx->stream>>>(logits, ids, weights, 1, experts, topk);
+        k_topk<<<ceil_div(tokens, 4), tokens == 1 ? 64 : 256, 0, ctx->stream>>>(logits, ids, weights, tokens, experts,
+                                                                             topk);
         return launched(ctx);
     }
     const int nrows = experts + (gate_w ? 1 : 0);
@@ -414,11 +503,18 @@ int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int exper
     const int nb = ceil_div(tokens, 64);
     DispatchWs w = dispatch_ws(tokens, experts);
     const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
+    GemmTiling none = {(int *)(ws + w.tile_small), (int *)(ws + w.tile_big), 64, 32, 128};
+    const GemmTiling &tl = tiling ? *tiling : none;
+    if (nb == 1) {
+        k_dispatch_one<<<1, SCAN_THREADS, 0, ctx->stream>>>(ids, tokens, topk, experts, offsets, rows, parts, where_,
+                                                            (int)extra, tl.small, tl.big, tl.split, tl.mt_small,
+                                                            tl.mt_big, (uint32_t *)(ws + w.status),
+                                                            (int4 *)tl.info_small, (int4 *)tl.info_big);
+        return launched(ctx);
+    }
     k_dispatch_masks<<<nb, 256, 0, ctx->stream>>>(ids, tokens, topk, experts, nb, (unsigned long long *)(ws + w.masks),
                                                   (int *)(ws + w.counts), (uint32_t *)(ws + w.flags));
     if (int rc = launched(ctx)) return rc;
-    GemmTiling none = {(int *)(ws + w.tile_small), (int *)(ws + w.tile_big), 64, 32, 128};
-    const GemmTiling &tl = tiling ? *tiling : none;
     k_dispatch_scan<<<1, SCAN_THREADS, 0, ctx->stream>>>((const int *)(ws + w.counts), (int *)(ws + w.base), offsets,
                                                  tl.small, tl.big, experts, nb, (int)extra, tl.split, tl.mt_small,
                                                  tl.mt_big, (const uint32_t *)(ws + w.flags),
