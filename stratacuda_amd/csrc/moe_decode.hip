@@ -349,7 +349,7 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
     float l0 = 0.0f, l1 = 0.0f;
     if (k < topk && !routed) sm::router_load(logits, experts, l0, l1);
     XQ first;
-    if (gl < width / 64) load_xq(xq, gl, first);
+    load_xq(xq, min(gl, width / 64 - 1), first);  // unconditional: the wait for the logits leaves these in flight
     sm::fill_exp_table(s_tab);
     if (k < topk && routed) {
         if (threadIdx.x == 0) s_ids[k] = ids[k];

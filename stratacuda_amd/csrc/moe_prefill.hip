@@ -731,10 +731,21 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, co
 constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
+// Batches of up to kSmallBatch tokens tile every segment (at most `tokens`
+// rows) in 16-row tiles, so the 64-row grid is not launched; larger ones
+// tile segments of more than 32 rows in 64-row tiles.
+constexpr int kSmallBatch = 64;
+inline int tiling_split(int tokens) { return tokens <= kSmallBatch ? kSmallBatch + 1 : 33; }
+
 // Grid bounds of the two tilings over the experts + 1 segments of m rows:
-// segments of up to 32 rows take at most two tiles; longer ones
-// ceil(rows / 64), i.e. at most m / 64 + (number of such segments <= m / 33).
-inline uint64_t small_tile_bound(int experts) { return 2 * ((uint64_t)experts + 1) + 1; }
+// a segment of r < split rows takes ceil(r / 16) <= r / 16 + 1 small tiles
+// (at most two when split is 33); a longer one ceil(r / 64) big tiles, in
+// all at most m / 64 + (number of such segments <= m / 33).
+inline uint64_t small_tile_bound(uint64_t m, int experts, int split) {
+    const uint64_t segs = (uint64_t)experts + 1;
+    const uint64_t any = m / 16 + std::min(segs, m) + 1;
+    return split <= 33 ? std::min(any, 2 * segs + 1) : any;
+}
 inline uint64_t big_tile_bound(uint64_t m, int experts) {
     return m / 64 + std::min((uint64_t)experts + 1, m / 33) + 1;
 }
@@ -753,7 +764,7 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool 
     w.tiles_small = up(w.offsets + ((uint64_t)experts + 2) * 4);
     w.tiles_big = up(w.tiles_small + ((uint64_t)experts + 2) * 4);
     w.info_small = up(w.tiles_big + ((uint64_t)experts + 2) * 4);
-    w.info_big = up(w.info_small + small_tile_bound(experts) * 16);
+    w.info_big = up(w.info_small + small_tile_bound(m, experts, tiling_split(tokens)) * 16);
     w.rows = up(w.info_big + big_tile_bound(m, experts) * 16);
     w.parts = up(w.rows + m * 4);
     w.where_ = up(w.parts + m * 4);
@@ -811,7 +822,8 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && (width == 2048 || width == 512) &&
                         (ff == 2048 || ff == 512);
     const int4 *info_small = (const int4 *)(ws + w.info_small), *info_big = (const int4 *)(ws + w.info_big);
-    GemmTiling tiling = {tiles_small, tiles_big, 33, stream ? 16 : 32, 64};
+    const int split = stream ? tiling_split(tokens) : 33;
+    GemmTiling tiling = {tiles_small, tiles_big, split, stream ? 16 : 32, 64};
     tiling.info_small = (int *)info_small;
     tiling.info_big = (int *)info_big;
     int rc = launched(ctx);
@@ -823,10 +835,11 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     if (rc_join) return rc_join;
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const uint64_t segs = (uint64_t)experts + 1;
-    // Segment tilings: > 32 rows in 64-row tiles ("big"), <= 32 rows in
+    // Segment tilings: `split` or more rows in 64-row tiles ("big"), fewer in
     // 16-row tiles (streaming kernels) or one 32-row tile (k_moe_gemm).
     const unsigned big_tiles = (unsigned)big_tile_bound(m, experts);
-    const unsigned small_tiles = (unsigned)(stream ? small_tile_bound(experts) : segs + 1);
+    const unsigned small_tiles = (unsigned)(stream ? small_tile_bound(m, experts, split) : segs + 1);
+    const bool any_big = split <= 33;  // otherwise no segment reaches the big tiling
     const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
     const int *rows = (const int *)(ws + w.rows);
     const uint8_t *ar = (const uint8_t *)arena, *sh = (const uint8_t *)shared_blob;
@@ -838,10 +851,13 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
             // The two tilings cover disjoint rows: the big-tile grid (few,
             // long blocks at small T) runs on the second stream beside the
             // small-tile grid.
-            if (int rc = fork_aux(ctx)) return rc;
-            kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(a, r, info_big, tiles_big, ar, blob_stride,
-                                                                          sh, experts, codes, scales, K, N, out, ld);
-            const int rc_big = launched(ctx);
+            int rc_big = SM_OK;
+            if (any_big) {
+                if (int rc = fork_aux(ctx)) return rc;
+                kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(
+                    a, r, info_big, tiles_big, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
+                rc_big = launched(ctx);
+            }
             auto ks = gate_up ? (K == 2048 ? k_moe_gemm_stream16<true, 32> : k_moe_gemm_stream16<true, 8>)
                               : (K == 2048 ? k_moe_gemm_stream16<false, 32> : k_moe_gemm_stream16<false, 8>);
             int rc_small = SM_OK;
@@ -850,7 +866,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                     a, r, info_small, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
                 rc_small = launched(ctx);
             }
-            const int rc_join = join_aux(ctx);
+            const int rc_join = any_big ? join_aux(ctx) : SM_OK;
             return rc_big ? rc_big : rc_small ? rc_small : rc_join;
         }
         if (N % 512 == 0) {

@@ -418,14 +418,17 @@ __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, 
         base += __popcll(m);
     }
     wave_lds_sync();
-    if (lane < count) {
-        const uint64_t q = x.cand[lane];
-        int rank = 0;
-        for (int m = 0; m < count; m++) rank += x.cand[m] > q ? 1 : 0;
-        if (rank < topK) {
-            x.ids[rank] = 511 - (int)(q & 511u);
-            x.val[rank] = __builtin_bit_cast(float, (uint32_t)(q >> 9) ^ 0x80000000u);
-        }
+    // Candidate `lane` against every candidate, read from its lane.
+    const uint64_t q = lane < count ? x.cand[lane] : 0ull;
+    int rank = 0;
+    for (int m = 0; m < count; m++) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)q, m);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(q >> 32), m);
+        rank += (((uint64_t)hi << 32) | lo) > q ? 1 : 0;
+    }
+    if (lane < count && rank < topK) {
+        x.ids[rank] = 511 - (int)(q & 511u);
+        x.val[rank] = __builtin_bit_cast(float, (uint32_t)(q >> 9) ^ 0x80000000u);
     }
     wave_lds_sync();
     mine = 0.0f;
@@ -443,8 +446,11 @@ __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, 
 // loads, as vector loads complete in order.
 __device__ __forceinline__ void router_load(const float *Logits, int experts, float &l0, float &l1) {
     const int e0 = threadIdx.x, e1 = threadIdx.x + 256;
-    l0 = e0 < experts ? Logits[e0] : -3.402823e38f;
-    l1 = e1 < experts ? Logits[e1] : -3.402823e38f;
+    // unconditional loads (clamped index), so a later wait can cover
+    // exactly these two
+    const float v0 = Logits[min(e0, experts - 1)], v1 = Logits[min(e1, experts - 1)];
+    l0 = e0 < experts ? v0 : -3.402823e38f;
+    l1 = e1 < experts ? v1 : -3.402823e38f;
 }
 __device__ __forceinline__ void router_block(float l0, float l1, int experts, int topK, const uint64_t *s_tab,
                                              RouterScratch &s, int *s_ids, float *s_w) {
@@ -454,21 +460,18 @@ __device__ __forceinline__ void router_block(float l0, float l1, int experts, in
     if (lane == 0) s.red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(s.red[0], s.red[1]), fmaxf(s.red[2], s.red[3]));
-    if (e0 < experts) s.p[e0] = expf_or(l0 - mx, s_tab);
-    if (e1 < experts) s.p[e1] = expf_or(l1 - mx, s_tab);
+    // Entries past `experts` hold +0: adding them to the (non-negative or
+    // NaN) sums below changes nothing, so wave 0 reads all eight at once.
+    s.p[e0] = e0 < experts ? expf_or(l0 - mx, s_tab) : 0.0f;
+    s.p[e1] = e1 < experts ? expf_or(l1 - mx, s_tab) : 0.0f;
     __syncthreads();
     if (wave != 0) return;
     float p[8];
     float sum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int e = lane + 64 * j;
-        p[j] = 0.0f;
-        if (e < experts) {
-            p[j] = s.p[e];
-            sum = sum + p[j];
-        }
-    }
+    for (int j = 0; j < 8; j++) p[j] = s.p[lane + 64 * j];
+#pragma unroll
+    for (int j = 0; j < 8; j++) sum = sum + p[j];
     sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tree_sum64(sum))));
     const float inv = 1.0f / sum;
     int key[8];

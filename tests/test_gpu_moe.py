@@ -179,6 +179,69 @@ def test_layer_prefill_2048_zipf_full(backend, oracle, full_layer):
     check_full_layer(backend, oracle, full_layer, 2048, True, 24)
 
 
+def routing_styles(E):
+    x = np.arange(E)
+    styles = {"ties": np.full(E, 7, np.float32),
+              "spread": (np.sin(x * 3.1) * 90).astype(np.float32),  # most probabilities underflow to 0
+              "pairs": np.repeat(np.random.default_rng(3).normal(0, 1, E // 2), 2).astype(np.float32)}
+    v = np.random.default_rng(5).normal(0, 1, E).astype(np.float32)
+    styles["nan_one"] = v.copy()
+    styles["nan_one"][3] = np.nan
+    styles["neg_inf_tail"] = v.copy()
+    styles["neg_inf_tail"][5:] = -np.inf
+    styles["pos_inf"] = v.copy()
+    styles["pos_inf"][100] = np.inf
+    styles["one_finite"] = np.full(E, -np.inf, np.float32)
+    styles["one_finite"][7] = 0.0
+    return styles
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 8, 20])
+def test_layer_routing_edge_logits(backend, oracle, full_layer, tokens):
+    # W_r = 0 makes every logit exactly the per-expert bias, so the layer's
+    # routing (the in-block top-k up to 4 tokens, the top-k kernel up to 16,
+    # the prefill router beyond) sees ties, underflow to 0, NaN and +-inf.
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    Wr0 = backend.alloc(np.zeros(E * W, np.float32))
+    X = device_inputs(backend, tokens, W, 77 + tokens, False)
+    Y, ids, w = backend.alloc(tokens * W), backend.alloc(tokens * K, "i32"), backend.alloc(tokens * K)
+    ws = backend.alloc_bytes(backend.moe_workspace_bytes(tokens, W, F, E, K))
+    for name, b in routing_styles(E).items():
+        backend.moe_layer(X, tokens, Wr0, full_layer.arena, full_layer.stride, full_layer.shared, full_layer.Wsg, W,
+                          F, E, K, Y, ids, w, ws, bias=backend.alloc(b))
+        rids, rw = oracle.router(np.tile(b, tokens), E, K, tokens)
+        assert np.array_equal(backend.read(ids), rids), name
+        assert same_bits(backend.read(w), rw), name
+
+
+@pytest.mark.parametrize("tokens", [17, 40, 64, 65])
+def test_layer_small_batch_full(backend, oracle, full_layer, tokens):
+    # 17..64 tokens: 16-row tiles over every segment with K split across
+    # blocks; 65: the first batch with 64-row tiles and no split.
+    check_full_layer(backend, oracle, full_layer, tokens, False, 6)
+
+
+@pytest.mark.parametrize("W,F,E,topk,tokens", [(512, 512, 24, 4, 40), (2048, 2048, 8, 2, 33),
+                                               (512, 2048, 12, 3, 100), (2048, 512, 20, 4, 48)])
+def test_layer_stream_geometries(backend, oracle, W, F, E, topk, tokens):
+    # Every (width, ff) pair of the streaming kernels, with and without the
+    # K split, against the oracle on all tokens.
+    layer = wl.DeviceLayer(backend, layer=0, width=W, ff=F, experts=E, base_seed=23)
+    host = wl.host_layer(oracle, 0, width=W, ff=F, experts=E, base_seed=23)
+    X = device_inputs(backend, tokens, W, 31 + tokens, False)
+    Y, ids, w = backend.alloc(tokens * W), backend.alloc(tokens * topk, "i32"), backend.alloc(tokens * topk)
+    ws = backend.alloc_bytes(backend.moe_workspace_bytes(tokens, W, F, E, topk))
+    backend.moe_layer(X, tokens, layer.Wr, layer.arena, layer.stride, layer.shared, layer.Wsg, W, F, E, topk, Y, ids,
+                      w, ws)
+    eY, eids, ew = oracle.moe_layer(backend.read(X), tokens, host["Wr"], host["arena"], host["stride"],
+                                    host["shared"], host["Wsg"], W, F, E, topk)
+    layer.free()
+    assert np.array_equal(backend.read(ids), eids)
+    assert same_bits(backend.read(w), ew)
+    got = backend.read(Y)
+    assert tol_ok(got, eY), "max abs err %g" % np.abs(got - eY).max()
+
+
 def test_layer_rejects_bad_arguments(backend, small):
     layer, _ = small
     W, F, E, K = 128, 64, 16, 4
