@@ -363,6 +363,34 @@ napi_value MoeLayer(napi_env env, napi_callback_info info) {
         return nullptr;
     return undefined(env);
 }
+napi_value MoeBlockWorkspace(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!a.need(5)) return nullptr;
+    int t = a.i32(0), w = a.i32(1), f = a.i32(2), e = a.i32(3), k = a.i32(4);
+    if (!a.ok) return nullptr;
+    uint64_t n = 0;
+    if (fail(env, nullptr, sm_moe_block_workspace(t, w, f, e, k, &n))) return nullptr;
+    return number(env, (double)n);
+}
+// moeBlock(ctx, H, tokens, gamma, eps, Wr, bias, arena, stride, shared, Wsg,
+//          width, ff, experts, topk, Hout, ids, weights, workspace, workspaceBytes)
+napi_value MoeBlock(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!a.need(20)) return nullptr;
+    sm_ctx *ctx = a.ctx(0);
+    uint64_t H = a.u64(1);
+    int tokens = a.i32(2);
+    uint64_t gamma = a.u64(3);
+    const float eps = (float)a.num(4);
+    uint64_t Wr = a.u64(5), bias = a.u64(6), arena = a.u64(7), stride = a.u64(8), shared = a.u64(9), Wsg = a.u64(10);
+    int width = a.i32(11), ff = a.i32(12), experts = a.i32(13), topk = a.i32(14);
+    uint64_t Hout = a.u64(15), ids = a.u64(16), weights = a.u64(17), ws = a.u64(18), wsb = a.u64(19);
+    if (!a.ok) return nullptr;
+    if (fail(env, ctx, sm_moe_block(ctx, H, tokens, gamma, eps, Wr, bias, arena, stride, shared, Wsg, width, ff, experts,
+                                    topk, Hout, ids, weights, ws, wsb)))
+        return nullptr;
+    return undefined(env);
+}
 // moeRoute(ctx, X, tokens, width, Wr, bias, experts, topk, logits, ids, weights)
 napi_value MoeRoute(napi_env env, napi_callback_info info) {
     Args a(env, info);
@@ -494,6 +522,8 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
                {"run", Run},
                {"moeWorkspace", MoeWorkspace},
                {"moeLayer", MoeLayer},
+               {"moeBlockWorkspace", MoeBlockWorkspace},
+               {"moeBlock", MoeBlock},
                {"moeRoute", MoeRoute},
                {"moeDispatch", MoeDispatch},
                {"synthNormal", SynthNormal},

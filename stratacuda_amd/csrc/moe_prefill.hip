@@ -622,19 +622,25 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
     for (int q = 0; q < NS - 1; q++) with_stage<BM>(q, [&](Stage &sg) { issue(sg, min(q, G - 1)); });
 
     const PairMagic magic = pair_magic();
-    const uint32_t shift = 8 * (kq & 1);
+    // Byte selector of the lane's code word: word x (kq < 2) or y, moved
+    // down by one byte for odd kq (v_perm_b32: 0-3 pick bytes of the second
+    // source, 4-7 of the first, 0x0c gives zero).
+    const uint32_t psel = kq == 0 ? 0x03020100u : kq == 1 ? 0x0c030201u : kq == 2 ? 0x07060504u : 0x0c070605u;
     float4v acc[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) acc[nt] = (float4v){0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute = [&](const Stage &sg, int g) {
         uint32_t words[NT][2];  // the lane's code word of step 0 and 1, shifted
-        half2v scale[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const v4u cv = sg.b[wave * 64 + nt * 16 + col];
-            words[nt][0] = (kq & 2 ? cv.y : cv.x) >> shift;
-            words[nt][1] = (kq & 2 ? cv.w : cv.z) >> shift;
+            words[nt][0] = __builtin_amdgcn_perm(cv.y, cv.x, psel);
+            words[nt][1] = __builtin_amdgcn_perm(cv.w, cv.z, psel);
+        }
+        half2v scale[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
             const uint16_t s16 = (uint16_t)(sreg[nt][g >> 1] >> (16 * (g & 1)));
             const _Float16 sh = __builtin_bit_cast(_Float16, s16);
             scale[nt] = (half2v){sh, sh};

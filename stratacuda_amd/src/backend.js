@@ -234,6 +234,22 @@ export class HipBackend {
             a.workspace.byteLength);
         this.dispatches++;
     }
+    moeBlockWorkspaceBytes(tokens, width, ff, experts, topK) {
+        return this.addon.moeBlockWorkspace(tokens, width, ff, experts, topK);
+    }
+    // One block of a stacked decoder around the MoE stage (strata_norm mode 0,
+    // the stage, strata_elementwise mode 5): Hout = H + MoE(RMSNorm(H; gamma)).
+    // Hout may be H itself. Bit-identical to the three steps run separately.
+    moeBlock(a) {
+        this.assertAlive();
+        const ws = this.owned(a.workspace, 'workspace');
+        this.addon.moeBlock(this.ctx, this.owned(a.H, 'H'), a.tokens, this.owned(a.gamma, 'gamma'), a.eps,
+            this.owned(a.Wr, 'Wr'), a.bias ? this.owned(a.bias, 'bias') : 0, this.owned(a.arena, 'arena'), a.stride,
+            this.owned(a.shared, 'shared'), this.owned(a.Wsg, 'Wsg'), a.width, a.ff, a.experts, a.topK,
+            this.owned(a.Hout, 'Hout'), this.owned(a.ids, 'ids'), this.owned(a.weights, 'weights'), ws,
+            a.workspace.byteLength);
+        this.dispatches++;
+    }
     moeRoute(a) {
         this.assertAlive();
         this.addon.moeRoute(this.ctx, this.owned(a.X, 'X'), a.tokens, a.width, this.owned(a.Wr, 'Wr'),

@@ -95,6 +95,25 @@ export class Ops {
             weights, workspace: this.workspace});
         return {y, ids, weights};
     }
+    // One stacked-decoder block on the device (kind 'hip'): h + MoE(RMSNorm(h;
+    // the layer's ffn_norm gamma, eps 1e-6)) in one call, with the routed ids
+    // and weights. The same bits as norm(), moe() and elem(.., 5) in turn.
+    async moeBlock(layer, h, tokens, options) {
+        tokens = tokens || 1;
+        const o = options || {}, g = this.store.config, entry = this.residency.layer(layer);
+        if (h.length !== tokens * g.width) throw Error('MoE input must hold tokens x width values');
+        const bytes = this.b.moeBlockWorkspaceBytes(tokens, g.width, g.ff, g.experts, g.topK);
+        if (!this.workspace || this.workspace.byteLength < bytes) {
+            if (this.workspace) this.b.free(this.workspace);
+            this.workspace = this.b.allocBytes(Math.ceil(bytes / 4) * 4, 'u32', {zero: false});
+        }
+        const out = o.output || await this.alloc(tokens * g.width), ids = await this.alloc(tokens * g.topK, 'i32');
+        const weights = await this.alloc(tokens * g.topK);
+        this.b.moeBlock({H: h, tokens, gamma: entry.gamma, eps: 1e-6, Wr: entry.Wr, bias: o.bias || null,
+            arena: entry.arena, stride: this.store.stride, shared: entry.shared, Wsg: entry.Wsg, width: g.width, ff: g.ff,
+            experts: g.experts, topK: g.topK, Hout: out, ids, weights, workspace: this.workspace});
+        return {h: out, ids, weights};
+    }
     async dispose() {
         await this.clearTemporary();
         if (this.residency) await this.residency.dispose();

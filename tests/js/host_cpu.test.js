@@ -39,6 +39,8 @@ function fakeAddon() {
         run: (ctx, name, groups, slots) => calls.push({name, groups, slots}),
         moeWorkspace: (...a) => real.moeWorkspace(...a),
         moeLayer: (ctx, ...args) => calls.push({name: 'moeLayer', args}),
+        moeBlockWorkspace: (...a) => real.moeBlockWorkspace(...a),
+        moeBlock: (ctx, ...args) => calls.push({name: 'moeBlock', args}),
         synthBlobs: (ctx, ...args) => calls.push({name: 'synthBlobs', args}),
         synthNormal: (ctx, ...args) => calls.push({name: 'synthNormal', args}),
         synthUniformPm: (ctx, ...args) => calls.push({name: 'synthUniformPm', args}),
@@ -47,7 +49,8 @@ function fakeAddon() {
 
 test('the addon exports every entry of the C ABI it wraps', () => {
     for (const f of ['init', 'shutdown', 'lastError', 'info', 'alloc', 'free', 'size', 'write', 'read', 'copy', 'zero',
-        'sync', 'kernels', 'signature', 'run', 'moeWorkspace', 'moeLayer', 'moeRoute', 'moeDispatch', 'synthNormal',
+        'sync', 'kernels', 'signature', 'run', 'moeWorkspace', 'moeLayer', 'moeBlockWorkspace', 'moeBlock', 'moeRoute',
+        'moeDispatch', 'synthNormal',
         'synthUniformPm', 'synthBlobs', 'eventRecord', 'eventElapsed', 'graphBegin', 'graphEnd', 'graphLaunch',
         'graphFree'])
         assert.strictEqual(typeof real[f], 'function', f);
@@ -196,6 +199,23 @@ test('MoE stage: kind hip runs the fused layer with the resident buffers', async
     assert.ok(call.args[16] >= real.moeWorkspace(3, 128, 64, 16, 4));
     await assert.rejects(stage.decode(0, x), /MoE input must hold tokens x width values/);
     assert.strictEqual(new MoeStage(ops, {fused: false}).fused, false);
+});
+
+test('moeBlock passes the layer gamma and the resident buffers in the C ABI order', async () => {
+    const addon = fakeAddon(), b = await HipBackend.create({addon});
+    const store = new SyntheticStore({width: 128, ff: 64, experts: 16, topK: 4});
+    const ops = new Ops(b, store), res = new WeightResidency(ops, [], 1 << 30);
+    const entry = await res.loadLayer(0), h = b.alloc(2 * 128);
+    addon.calls.length = 0;
+    const r = await ops.moeBlock(0, h, 2);
+    const call = addon.calls[0];
+    assert.strictEqual(call.name, 'moeBlock');
+    // H, tokens, gamma, eps, Wr, bias, arena, stride, shared, Wsg, width, ff, experts, topk, Hout, ids, weights, ws, wsBytes
+    assert.deepStrictEqual(call.args.slice(0, 14), [h.id, 2, entry.gamma.id, 1e-6, entry.Wr.id, 0, entry.arena.id, 6912,
+        entry.shared.id, entry.Wsg.id, 128, 64, 16, 4]);
+    assert.deepStrictEqual(call.args.slice(14, 17), [r.h.id, r.ids.id, r.weights.id]);
+    assert.ok(call.args[18] >= real.moeBlockWorkspace(2, 128, 64, 16, 4));
+    await assert.rejects(ops.moeBlock(0, h, 3), /MoE input must hold tokens x width values/);
 });
 
 run();

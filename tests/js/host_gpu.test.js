@@ -68,6 +68,27 @@ for (const c of manifest.cases) {
     }
 }
 
+// The block entry (one device call per stacked-decoder layer) against the
+// three host steps it replaces: strata_norm mode 0, the fused stage and
+// strata_elementwise mode 5, bit for bit.
+const full = manifest.cases.find(c => c.name === 'full_decode');
+for (const T of [1, 20]) {
+    test('moeBlock equals norm, moe and residual, ' + T + ' token(s)', async () => {
+        const c = Object.assign({}, full, {tokens: T, inputSeed: 300 + T});
+        const {ops, x} = await session(c);
+        const gamma = ops.residency.layer(0).gamma;
+        const xn = await ops.norm(x, gamma, c.width, T);
+        const r = await ops.moe(0, xn, T);
+        const ref = await ops.elem(x, r.y, 5);
+        const b = await ops.moeBlock(0, x, T);
+        await backend.idle();
+        assert.deepStrictEqual(bits(await backend.read(b.h)), bits(await backend.read(ref)));
+        assert.deepStrictEqual(Array.from(await backend.read(b.ids)), Array.from(await backend.read(r.ids)));
+        assert.deepStrictEqual(bits(await backend.read(b.weights)), bits(await backend.read(r.weights)));
+        await ops.dispose();
+    });
+}
+
 test('errors surface as exceptions, not faults', async () => {
     if (!backend) backend = await HipBackend.create({device: 0});
     const L = backend.alloc(513), ids = backend.alloc(10, 'i32'), w = backend.alloc(10);
