@@ -331,7 +331,6 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
                                                         int width, int ff, int topk, int experts, uint64_t gu_scales,
                                                         int routed) {
     __shared__ int s_ids[32];
-    __shared__ float s_w[32];
     __shared__ uint64_t s_tab[32];
     __shared__ sm::RouterScratch s_router;
     const int wave = threadIdx.x >> 6, gl = threadIdx.x & 31;
@@ -346,28 +345,28 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
     }
     // routed: the IDs are already in memory (a top-k kernel ran per token)
     // and the block reads its slot's ID instead of selecting it itself.
-    float l0 = 0.0f, l1 = 0.0f;
-    if (k < topk && !routed) sm::router_load(logits, experts, l0, l1);
+    float lg[8];
+    if (k < topk && !routed) sm::router_load(logits, experts, lg);
     XQ first;
     load_xq(xq, min(gl, width / 64 - 1), first);  // unconditional: the wait for the logits leaves these in flight
     sm::fill_exp_table(s_tab);
     if (k < topk && routed) {
         if (threadIdx.x == 0) s_ids[k] = ids[k];
-        __syncthreads();
     } else if (k < topk) {
-        sm::router_block(l0, l1, experts, topk, s_tab, s_router, s_ids, s_w);
-        __syncthreads();
-        if (blockIdx.x == 0 && k == 0 && (int)threadIdx.x < topk) {
-            ids[threadIdx.x] = s_ids[threadIdx.x];
-            weights[threadIdx.x] = s_w[threadIdx.x];
-        }
-    } else {
-        __syncthreads();
+        sm::router_block(lg, experts, topk, s_tab, s_router, s_ids);
     }
+    __syncthreads();
     const uint8_t *blob = slot_blob(arena, stride, shared_blob, k < topk ? s_ids[k] : 0, k, topk, experts);
     const int j0 = (blockIdx.x * GU_WAVES + wave) * GU_ROWS;
     if (j0 < ff)
         gate_up_rows(xq, first, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
+    // Block (0, 0) publishes the token's IDs and routing weights, after its
+    // own expert work so that no block's loads wait for the weights.
+    if (k == 0 && !routed && blockIdx.x == 0 && wave == 0) {
+        const int lane = threadIdx.x;
+        if (lane < topk) ids[lane] = s_ids[lane];
+        sm::router_weights(lane < topk ? s_router.val[lane] : 0.0f, topk, weights);
+    }
 }
 
 // K3, the combine at its end shared by both variants (kernels/strata.cu:360-365):

@@ -75,11 +75,13 @@ __device__ __forceinline__ float expf_or(float x, const uint64_t *tab = kExp2Tab
     y = y * s;
     return (float)y;
 }
-// Fills an LDS copy of kExp2Tab (threads 0-31, one entry each) from values
-// known at compile time: no vector-memory load, so nothing delays the
-// kernel's first loads.
+// Fills an LDS copy of kExp2Tab (lanes 0-31 of every wave, one entry each,
+// all waves writing the same values) from values known at compile time: no
+// vector-memory load, so nothing delays the kernel's first loads. A wave may
+// read the table after wave_lds_sync() (its own writes are then complete),
+// without waiting for the other waves.
 __device__ __forceinline__ void fill_exp_table(uint64_t *s_tab) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & 63;
     if (t < 32) {
         uint64_t v = kExp2Tab[0];
 #pragma unroll
@@ -368,7 +370,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 struct RouterScratch {
     float p[512];
     float red[4];
-    uint64_t cand[64];
+    uint64_t cand[128];  // 64 candidates + one discard slot per lane
     int ids[32];
     float val[32];
 };
@@ -377,53 +379,68 @@ struct RouterScratch {
 // order key Q = (key ^ 2^31) << 9 | (511 - e): Q descending is exactly the
 // order in which the reference's rounds pick experts (larger probability
 // first, lower ID on equal probabilities), so round k picks the entry of
-// rank k. The topK largest entries all have a key >= T, the topK-th largest
-// of the 64 lane maxima (those maxima are topK distinct entries); T comes
-// from a bitwise search with ballots. The entries with key >= T are gathered
-// in LDS (one per lane) and each is ranked against the others. With more
-// than 64 such entries (heavy ties), or when T belongs to an invalid entry
-// (no probability >= 0 among them: NaN routing input), the rounds of
-// select_rounds run instead.
+// rank k. Any threshold T at or below the topK-th largest of the 64 lane
+// maxima (those maxima are topK distinct entries) keeps every selected entry
+// among those with key >= T; a bitwise search with ballots sets T's upper
+// bits. The entries with key >= T are gathered in LDS (one per lane) and
+// each is ranked against the others. With more than 64 such entries (heavy
+// ties), or fewer than topK lanes holding a probability >= 0 (NaN routing
+// input), the rounds of select_rounds run instead.
 __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, int topK, RouterScratch &x,
                                               int *s_ids, float &mine) {
     const int lane = threadIdx.x & 63;
     uint32_t hk = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) hk = max(hk, (uint32_t)key[j] ^ 0x80000000u);
-    uint32_t T = 0;
+    // Every valid entry (p >= 0) has a key >= 2^31 here; fewer than topK
+    // lanes with one means NaN routing input or topK > 64.
+    if (__popcll(__ballot(hk >= 0x80000000u)) < topK) {
+        select_rounds(key, experts, topK, s_ids, mine);
+        return;
+    }
+    // Bits 29..16 of T (p <= 1 keeps bit 30 clear). Any T at or below the
+    // topK-th largest lane maximum is a valid threshold: the low bits only
+    // trim candidates, and with them unset the candidates are typically
+    // topK + 1 (measured on random logits: at most 17 for topK = 10).
+    uint32_t T = 0x80000000u;
 #pragma unroll
-    for (int b = 31; b >= 0; b--) {
+    for (int b = 29; b >= 16; b--) {
         const uint32_t c = T | (1u << b);
         if (__popcll(__ballot(hk >= c)) >= topK) T = c;
     }
-    int count = 0;
     uint64_t Q[8];
+    bool in[8];
+    unsigned long long mask[8];
+    int count = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const uint32_t k = (uint32_t)key[j] ^ 0x80000000u;
         Q[j] = ((uint64_t)k << 9) | (uint64_t)(511 - (lane + 64 * j));
-        count += __popcll(__ballot(k >= T));
+        in[j] = k >= T;
+        mask[j] = __ballot(in[j]);
+        count += __popcll(mask[j]);
     }
-    if (T < 0x80000000u || count > 64) {
+    if (count > 64) {
         select_rounds(key, experts, topK, s_ids, mine);
         return;
     }
+    // Gather: candidate i goes to cand[i]; entries below T to the lane's
+    // discard slot (no branches).
     int base = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const bool in = (uint32_t)(Q[j] >> 9) >= T;
-        const unsigned long long m = __ballot(in);
-        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-        if (in) x.cand[base + below] = Q[j];
-        base += __popcll(m);
+        const int below =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(mask[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask[j], 0));
+        x.cand[in[j] ? base + below : 64 + lane] = Q[j];
+        base += __popcll(mask[j]);
     }
     wave_lds_sync();
     // Candidate `lane` against every candidate, read from its lane.
     const uint64_t q = lane < count ? x.cand[lane] : 0ull;
     int rank = 0;
-    for (int m = 0; m < count; m++) {
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)q, m);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(q >> 32), m);
+    for (int c = 0; c < count; c++) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)q, c);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(q >> 32), c);
         rank += (((uint64_t)hi << 32) | lo) > q ? 1 : 0;
     }
     if (lane < count && rank < topK) {
@@ -440,26 +457,41 @@ __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, 
 
 // The same routing for one token by a 256-thread block: the 512 exponentials
 // are spread over all threads (table in LDS), wave 0 forms the reference sum
-// and runs the selection rounds. Results land in s_ids / s_w (LDS). Needs
+// and runs the selection. The IDs land in s_ids and the selected
+// probabilities in s.val[0, topK) (LDS; router_weights forms the weights). Needs
 // blockDim.x == 256 and experts <= 512. s_tab must already hold kExp2Tab.
 // Thread t's logits (experts t and t + 256); issued before a kernel's other
 // loads, as vector loads complete in order.
-__device__ __forceinline__ void router_load(const float *Logits, int experts, float &l0, float &l1) {
-    const int e0 = threadIdx.x, e1 = threadIdx.x + 256;
-    // unconditional loads (clamped index), so a later wait can cover
-    // exactly these two
-    const float v0 = Logits[min(e0, experts - 1)], v1 = Logits[min(e1, experts - 1)];
-    l0 = e0 < experts ? v0 : -3.402823e38f;
-    l1 = e1 < experts ? v1 : -3.402823e38f;
+// Every wave loads all the token's logits (lane l: experts l + 64 j; past
+// `experts`: -FLT_MAX), so each forms the maximum itself, with no barrier.
+// Unconditional loads (clamped index), so a later wait covers exactly these.
+__device__ __forceinline__ void router_load(const float *Logits, int experts, float (&l)[8]) {
+    const int lane = threadIdx.x & 63;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = Logits[min(lane + 64 * j, experts - 1)];
+#pragma unroll
+    for (int j = 0; j < 8; j++) l[j] = lane + 64 * j < experts ? v[j] : -3.402823e38f;
 }
-__device__ __forceinline__ void router_block(float l0, float l1, int experts, int topK, const uint64_t *s_tab,
-                                             RouterScratch &s, int *s_ids, float *s_w) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void router_block(const float (&l)[8], int experts, int topK, const uint64_t *s_tab,
+                                             RouterScratch &s, int *s_ids) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int e0 = tid, e1 = tid + 256;
-    float mx = wave_max(fmaxf(l0, l1));
-    if (lane == 0) s.red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(s.red[0], s.red[1]), fmaxf(s.red[2], s.red[3]));
+    // fmaxf returns one of its operands, so the order of the maximum does
+    // not change its value
+    float mx = l[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) mx = fmaxf(mx, l[j]);
+    mx = wave_max(mx);
+    wave_lds_sync();  // this wave's copy of the exp table is in LDS
+    float l0 = l[0], l1 = l[4];  // experts e0 = lane + 64 wave and e1 = e0 + 256
+#pragma unroll
+    for (int j = 1; j < 4; j++)
+        if (wave == j) {
+            l0 = l[j];
+            l1 = l[j + 4];
+        }
     // Entries past `experts` hold +0: adding them to the (non-negative or
     // NaN) sums below changes nothing, so wave 0 reads all eight at once.
     s.p[e0] = e0 < experts ? expf_or(l0 - mx, s_tab) : 0.0f;
@@ -479,7 +511,9 @@ __device__ __forceinline__ void router_block(float l0, float l1, int experts, in
     for (int j = 0; j < 8; j++) key[j] = select_key(p[j] * inv, lane + 64 * j < experts);
     float mine;
     select_ranked(key, experts, topK, s, s_ids, mine);
-    router_weights(mine, topK, s_w);
+    // The selected probabilities, for router_weights once the block has
+    // issued its expert loads (the IDs alone gate those).
+    if (lane < topK) s.val[lane] = mine;
 }
 
 }  // namespace sm
