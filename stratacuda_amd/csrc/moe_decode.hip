@@ -372,16 +372,39 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
 // K3, the combine at its end shared by both variants (kernels/strata.cu:360-365):
 // y = shared * sigmoid(gate) + sum_k part_k * w_k, in that order.
 // With `resid`, Y = resid + y (strata_elementwise mode 5, scale 1).
-__device__ __forceinline__ void down_combine(const float *parts, const float *__restrict__ weights,
-                                             const float *__restrict__ gate, float *__restrict__ Y, int width,
-                                             int topk, const uint64_t *s_tab, const float *__restrict__ resid) {
+// Its inputs do not depend on the expert work, so they are loaded when the
+// kernel starts (unconditional loads on valid addresses) and the tail after
+// the last barrier makes no memory round trip: thread k < topk holds w_k,
+// threads < 8 the gate and the residual of their row.
+struct CombineIn {
+    float w, gate, res;
+};
+__device__ __forceinline__ CombineIn combine_load(const float *__restrict__ weights, const float *__restrict__ gate,
+                                                  const float *__restrict__ resid, int width, int topk) {
+    const int tid = threadIdx.x;
+    const int row = min((int)blockIdx.x * 8 + (tid & 7), width - 1);
+    CombineIn in;
+    in.w = weights[min(tid, topk - 1)];
+    in.gate = gate[0];
+    in.res = *(resid ? resid + row : gate);
+    return in;
+}
+// Before the last barrier: the weights into LDS and, in the combining
+// threads, sigmoid(gate) (s_tab must hold this wave's copy of the table).
+__device__ __forceinline__ float combine_stage(const CombineIn &in, float *s_w, int topk, const uint64_t *s_tab) {
+    const int tid = threadIdx.x;
+    if (tid < topk) s_w[tid] = in.w;
+    return tid < 8 ? sm::sigmoid(in.gate, s_tab) : 0.0f;
+}
+__device__ __forceinline__ void down_combine(const float *parts, const float *s_w, float sig, const CombineIn &in,
+                                             float *__restrict__ Y, int width, int topk, bool has_resid) {
     const int tid = threadIdx.x;
     if (tid < 8) {
         const int row = blockIdx.x * 8 + tid;
         if (row < width) {
-            float value = parts[topk * 8 + tid] * sm::sigmoid(gate[0], s_tab);
-            for (int k = 0; k < topk; k++) value = value + parts[k * 8 + tid] * weights[k];
-            Y[row] = resid ? resid[row] + value : value;
+            float value = parts[topk * 8 + tid] * sig;
+            for (int k = 0; k < topk; k++) value = value + parts[k * 8 + tid] * s_w[k];
+            Y[row] = has_resid ? in.res + value : value;
         }
     }
 }
@@ -420,6 +443,7 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
         if (resid) resid += (int64_t)t * width;
     }
     __shared__ float parts[33 * 8];
+    __shared__ float s_w[32];
     __shared__ uint64_t s_tab[32];
     __shared__ __attribute__((aligned(16))) float s_h[DN_WAVES][8 * DN_PITCH];
     const int nexp = topk + 1, GF = ff / 64;
@@ -430,6 +454,7 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
     const int gc = min(gl, GF - 1);
     const uint64_t row_bytes = (uint64_t)ff / 4;
     const int my_id = ids[min(lane, topk - 1)];
+    const CombineIn cin = combine_load(weights, gate, resid, width, topk);
     // The lane's eighth (8 values) of its hidden group, for every slot.
     float4 hq[NQ][2];
 #pragma unroll
@@ -491,8 +516,9 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
         v = sm::group8_sum(v);
         if (gl == 0 && k < nexp) parts[k * 8 + rr] = v;
     }
+    const float sig = combine_stage(cin, s_w, topk, s_tab);
     __syncthreads();
-    down_combine(parts, weights, gate, Y, width, topk, s_tab, resid);
+    down_combine(parts, s_w, sig, cin, Y, width, topk, resid != nullptr);
 }
 
 // K3 for any other shape: hidden groups read from memory, lanes loop over
@@ -514,9 +540,11 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
         if (resid) resid += (int64_t)t * width;
     }
     __shared__ float parts[33 * 8];
+    __shared__ float s_w[32];
     __shared__ uint64_t s_tab[32];
     const int nexp = topk + 1, GF = ff / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const CombineIn cin = combine_load(weights, gate, resid, width, topk);
     sm::fill_exp_table(s_tab);
     const int r = min((int)blockIdx.x * 8 + (lane >> 3), width - 1), gl = lane & 7;
     const uint64_t row_bytes = (uint64_t)ff / 4;
@@ -535,8 +563,9 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
         v = sm::group8_sum(v);
         if (gl == 0) parts[k * 8 + (lane >> 3)] = v;
     }
+    const float sig = combine_stage(cin, s_w, topk, s_tab);
     __syncthreads();
-    down_combine(parts, weights, gate, Y, width, topk, s_tab, resid);
+    down_combine(parts, s_w, sig, cin, Y, width, topk, resid != nullptr);
 }
 
 constexpr uint64_t kAlign = 256;
