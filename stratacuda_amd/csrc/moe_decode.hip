@@ -235,14 +235,19 @@ __device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, co
             group(g, q);
         }
     }
+    // Row r's gate and up sums (lanes 31 and 63 after the half-wave sums)
+    // go to lane r, so the rows' SiLU run side by side and one store writes them.
+    float g = 0.0f, u = 0.0f;
 #pragma unroll
     for (int r = 0; r < GU_ROWS; r++) {
-        const float v = sm::half32_sum(acc[r]);  // lane 31: gate row, lane 63: up row
-        const float g = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
-        const float u = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-        const int j = j0 + r;
-        if (lane == 0 && j < ff) hidden_row[j] = blob ? sm::silu(g, tab) * u : __builtin_nanf("");
+        const float v = sm::half32_sum(acc[r]);
+        const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+        const float ur = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+        g = lane == r ? gr : g;
+        u = lane == r ? ur : u;
     }
+    const int j = j0 + lane;
+    if (lane < GU_ROWS && j < ff) hidden_row[j] = blob ? sm::silu(g, tab) * u : __builtin_nanf("");
 }
 
 // K1. Blocks [0, route_blocks): 4 router rows each (row `experts` = shared
