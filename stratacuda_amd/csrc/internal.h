@@ -105,7 +105,7 @@ struct BlockArgs {
 };
 // Batches of up to kDecodeMaxTokens tokens run the decode (GEMV) kernels with
 // a token dimension; larger ones the dispatch + grouped GEMM path.
-constexpr int kDecodeMaxTokens = 16;
+constexpr int kDecodeMaxTokens = 24;
 constexpr int kDecodeBlockRouting = 4;  // up to this many tokens the gate/up blocks route
 constexpr int kRouteRowsMaxTokens = 64;  // router logits one wave per (row, token) up to here
 // Exact per-token top-k (strata_router order) of logits [tokens x experts].
