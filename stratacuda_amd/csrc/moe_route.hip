@@ -162,15 +162,23 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
     }
 }
 
+// Top-k of every token's logits (kernels/strata.cu:479-509 strata_router_batch
+// results): one 256-thread block per token (router_block: the exponentials
+// over four waves, the ranked selection in wave 0). Needs experts <= 512.
 __global__ void __launch_bounds__(256) k_topk(const float *__restrict__ logits, int *__restrict__ ids,
-                                              float *__restrict__ weights, int tokens, int experts, int topk) {
+                                              float *__restrict__ weights, int experts, int topk) {
     __shared__ uint64_t s_tab[32];
+    __shared__ sm::RouterScratch s_router;
+    __shared__ int s_ids[32];
+    const int t = blockIdx.x;
+    float lg[8];
+    sm::router_load(logits + (int64_t)t * experts, experts, lg);
     sm::fill_exp_table(s_tab);
-    __syncthreads();
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= tokens) return;
-    sm::router_wave(logits + (int64_t)t * experts, ids + (int64_t)t * topk, weights + (int64_t)t * topk, experts, topk,
-                    s_tab);
+    sm::router_block(lg, experts, topk, s_tab, s_router, s_ids);  // waves 1-3 return inside
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    if (lane < topk) ids[(int64_t)t * topk + lane] = s_ids[lane];
+    sm::router_weights(lane < topk ? s_router.val[lane] : 0.0f, topk, weights + (int64_t)t * topk);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -439,7 +447,7 @@ namespace smi {
 uint64_t dispatch_workspace(int tokens, int experts) { return dispatch_ws(tokens, experts).end; }
 
 int topk_launch(sm_ctx *ctx, const float *logits, int *ids, float *weights, int tokens, int experts, int topk) {
-    k_topk<<<ceil_div(tokens, 4), 256, 0, ctx->stream>>>(logits, ids, weights, tokens, experts, topk);
+    k_topk<<<(unsigned)tokens, 256, 0, ctx->stream>>>(logits, ids, weights, experts, topk);
     return launched(ctx);
 }
 
@@ -456,16 +464,14 @@ int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float
             k_route_rows<0><<<grid, 64, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, width, experts,
                                                          total);
         if (int rc = launched(ctx)) return rc;
-        k_topk<<<ceil_div(tokens, 4), tokens == 1 ? 64 : 256, 0, ctx->stream>>>(logits, ids, weights, tokens, experts,
-                                                                             topk);
-        return launched(ctx);
+        return topk_launch(ctx, logits, ids, weights, tokens, experts, topk);
     }
     const int nrows = experts + (gate_w ? 1 : 0);
     dim3 grid((unsigned)ceil_div(ceil_div(nrows, TR), 4), (unsigned)ceil_div(tokens, TT));
     k_route_gemm<<<grid, 256, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, tokens, width, experts,
                                                 gate_w ? 1 : 0);
     if (int rc = launched(ctx)) return rc;
-    k_topk<<<ceil_div(tokens, 4), 256, 0, ctx->stream>>>(logits, ids, weights, tokens, experts, topk);
+    k_topk<<<(unsigned)tokens, 256, 0, ctx->stream>>>(logits, ids, weights, experts, topk);
     return launched(ctx);
 }
 
