@@ -75,6 +75,29 @@ def lib():
             "or_synth_blob": (None, [_u8p, _i, _i, _u64, _u64, ctypes.c_double]),
             "or_expf_survey": (None, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                       np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")]),
+            # strata_oracle_model.c: the fixture model's other kernels
+            "or_logf": (ctypes.c_float, [ctypes.c_float]),
+            "or_sinf": (ctypes.c_float, [ctypes.c_float]),
+            "or_cosf": (ctypes.c_float, [ctypes.c_float]),
+            "or_embedding": (None, [_vp, _vp, _vp, _vp, _f32p, _i, _i, _i, _i, _i, _i, _i, _i, _i]),
+            "or_rope_frequencies": (None, [_f32p, _f32p, _i, ctypes.c_float]),
+            "or_rope_table": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i]),
+            "or_rope_position": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _i]),
+            "or_hc_mix": (None, [_f32p, _f32p, _f32p, _i, _i]),
+            "or_hc_write": (None, [_f32p, _f32p, _f32p, _i, _i]),
+            "or_conv": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i]),
+            "or_gdn_gates": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i]),
+            "or_gdn_step": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i]),
+            "or_slice": (None, [_f32p, _f32p, _i, _i, _i, _i]),
+            "or_kv_append": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i]),
+            "or_attention": (None, [_f32p, _f32p, _f32p, _i32p, _f32p, _i, _i, _i, _i, ctypes.c_float]),
+            "or_attention_gate": (None, [_f32p, _f32p, _f32p, _i, _i]),
+            "or_ple_gate": (None, [_f32p, _f32p, _f32p, _i, _i]),
+            "or_ple_broadcast": (None, [_f32p, _f32p, _f32p, _i, _i]),
+            "or_ple_add": (None, [_f32p, _f32p, _f32p, _i]),
+            "or_argmax": (_i, [_f32p, _i]),
+            "or_math_survey": (None, [_i, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                      np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -293,3 +316,125 @@ def ref_dequant_table():
         subprocess.run([REF_DEQUANT, out], check=True)
         data = np.fromfile(out, dtype="<f4")
     return data[:65536], data[65536:].reshape(256, 64)
+
+
+# ------------------------------------------- fixture-model kernels (part 2)
+# Restatements of the kernels StrataEngine.step uses outside the MoE stage
+# (strata_oracle_model.c). Buffers the reference kernel updates in place
+# (Residual, History, State, Keys/Values) are float32 arrays updated in place.
+def logf(x):
+    return np.float32(lib().or_logf(float(np.float32(x))))
+
+
+def sinf(x):
+    return np.float32(lib().or_sinf(float(np.float32(x))))
+
+
+def cosf(x):
+    return np.float32(lib().or_cosf(float(np.float32(x))))
+
+
+def math_survey(fn, start_bits, end_bits, step=1):
+    """fn 0 logf, 1 sinf, 2 cosf: (mismatches vs libm, mismatches beyond one ulp)."""
+    out = np.zeros(2, np.uint64)
+    lib().or_math_survey({"logf": 0, "sinf": 1, "cosf": 2}[fn], start_bits, end_bits, step, out)
+    return int(out[0]), int(out[1])
+
+
+def embedding(residual, width, streams, values=None, codes=None, scales=None, offsets=None, output_offset=0,
+              fmt=0, bits=0, group_size=1, bias=0, codebook=0, has_offset=0):
+    keep = [None if a is None else (f32(a) if a is not codes else u32(a)) for a in (values, codes, scales, offsets)]
+    lib().or_embedding(*[_ptr(a) for a in keep], residual, width, streams, output_offset, fmt, bits, group_size,
+                       bias, codebook, has_offset)
+    return residual
+
+
+def rope_frequencies(rotary, base):
+    hi, lo = np.zeros(rotary // 2, np.float32), np.zeros(rotary // 2, np.float32)
+    lib().or_rope_frequencies(hi, lo, rotary, float(np.float32(base)))
+    return hi, lo
+
+
+def rope_table(hi, lo, rotary, context):
+    cos, sin = np.zeros(context * rotary // 2, np.float32), np.zeros(context * rotary // 2, np.float32)
+    lib().or_rope_table(f32(hi), f32(lo), cos, sin, rotary, context)
+    return cos, sin
+
+
+def rope_position(X, cos, sin, dim, heads, rotary, position, tokens=1):
+    Y = np.zeros(dim * heads * tokens, np.float32)
+    lib().or_rope_position(f32(X), f32(cos), f32(sin), Y, dim, heads, rotary, position, tokens)
+    return Y
+
+
+def hc_mix(norm_, gate, width, streams):
+    out = np.zeros(width, np.float32)
+    lib().or_hc_mix(f32(norm_), f32(gate), out, width, streams)
+    return out
+
+
+def hc_write(residual, output, inject, width, streams):
+    lib().or_hc_write(residual, f32(output), f32(inject), width, streams)
+    return residual
+
+
+def conv(history, X, W, channels, taps, dilation, activation=1):
+    Y = np.zeros(channels, np.float32)
+    lib().or_conv(history, f32(X), f32(W), Y, channels, taps, dilation, activation)
+    return Y
+
+
+def gdn_gates(alpha, beta, A, dt, heads):
+    decay, strength = np.zeros(heads, np.float32), np.zeros(heads, np.float32)
+    lib().or_gdn_gates(f32(alpha), f32(beta), f32(A), f32(dt), decay, strength, heads)
+    return decay, strength
+
+
+def gdn_step(state, q, k, v, decay, beta, dim, key_heads, value_heads):
+    Y = np.zeros(dim * value_heads, np.float32)
+    lib().or_gdn_step(state, f32(q), f32(k), f32(v), f32(decay), f32(beta), Y, dim, key_heads, value_heads)
+    return Y
+
+
+def slice_(X, width, rows=1, stride=None, offset=0):
+    Y = np.zeros(width * rows, np.float32)
+    lib().or_slice(f32(X), Y, width, rows, width if stride is None else stride, offset)
+    return Y
+
+
+def kv_append(k, v, keys, values, width, position):
+    lib().or_kv_append(f32(k), f32(v), keys, values, width, position)
+
+
+def attention(Q, keys, values, cells, dim, heads, kv_heads, count, scale):
+    Y = np.zeros(dim * heads, np.float32)
+    lib().or_attention(f32(Q), f32(keys), f32(values), i32(cells), Y, dim, heads, kv_heads, count,
+                       float(np.float32(scale)))
+    return Y
+
+
+def attention_gate(attn, full_q, dim, heads):
+    Y = np.zeros(dim * heads, np.float32)
+    lib().or_attention_gate(f32(attn), f32(full_q), Y, dim, heads)
+    return Y
+
+
+def ple_gate(key, query, width, streams):
+    gate = np.zeros(streams, np.float32)
+    lib().or_ple_gate(f32(key), f32(query), gate, width, streams)
+    return gate
+
+
+def ple_broadcast(value, gate, width, streams):
+    Y = np.zeros(width * streams, np.float32)
+    lib().or_ple_broadcast(f32(value), f32(gate), Y, width, streams)
+    return Y
+
+
+def ple_add(residual, gated, conv_, n):
+    lib().or_ple_add(residual, f32(gated), f32(conv_), n)
+    return residual
+
+
+def argmax(logits, count):
+    return int(lib().or_argmax(f32(logits), count))
