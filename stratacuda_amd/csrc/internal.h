@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 #include <map>
 #include <string>
@@ -123,6 +124,39 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
 uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk, bool block = false);
 // strata_norm mode 0 (scale 1) over `rows` rows of `cols`, on the context's stream.
 int norm_launch(sm_ctx *ctx, const float *X, const float *gamma, float *Y, int cols, int rows, float eps);
+
+// ------------------------------------------------ kernels by name (sm_run)
+// One 64-bit slot per reference parameter: a buffer handle, or the int32 /
+// float32 bit pattern in the low 32 bits.
+struct Args {
+    const uint64_t *a;
+    uint64_t ptr(int i) const { return a[i]; }
+    int i32(int i) const { return (int)(uint32_t)(a[i] & 0xffffffffu); }
+    float f32(int i) const {
+        uint32_t u = (uint32_t)(a[i] & 0xffffffffu);
+        float f;
+        memcpy(&f, &u, 4);
+        return f;
+    }
+};
+// A launcher validates the arguments and every buffer access of the grid
+// (G = workgroups of 64 lanes), then launches on ctx->stream.
+typedef int (*Launcher)(sm_ctx *, const uint32_t *G, Args);
+struct Entry {
+    const char *name;
+    const char *signature;  // "Name:type,..." in the reference's parameter order
+    int nargs;
+    Launcher launch;
+};
+// The fixture model's kernels outside the MoE path (kernels_model.hip).
+const Entry *model_entries(int *count);
+// Recorded size of a live buffer handle in bytes, -1 when it is not one.
+int64_t buf_len(sm_ctx *ctx, uint64_t handle);
+// Checks on the device that idx[first + i*stride], i < n, lie in [lo, hi):
+// the host cannot see device-resident indices. Synchronises the stream;
+// refused while capturing.
+int check_indices(sm_ctx *ctx, uint64_t buf, int64_t n, int64_t stride, int64_t first, int lo, int hi,
+                  const char *what);
 
 // Byte sizes of the regions of one Q2 expert blob.
 struct BlobLayout {

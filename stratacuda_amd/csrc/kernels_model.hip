@@ -1,0 +1,579 @@
+// The untrained fixture model's kernels outside the MoE path, by reference
+// name for sm_run (backend.run(name, args, groups)): what StrataEngine.step
+// (src/engine.js:76-196) launches besides the router, the projections, the
+// norm, the elementwise modes and the combine.
+//
+// Each kernel computes what the kernels/strata.cu entry of the same name
+// computes, in the same f32 (and, for RoPE, f64) operation order, so results
+// are bit-identical to the CPU oracle. Kernels of one work item per lane use
+// 256-thread blocks over the items the 64-lane grid covers; the three
+// reductions (attention, PLE gate, argmax) run one reference workgroup as one
+// 64-lane wavefront, the reference's shared-memory trees becoming cross-lane
+// shuffles in the same order.
+//
+// Launchers check the reference's validateDispatch conditions
+// (src/backend.js:33-55) and then every buffer access of the requested grid
+// against the recorded allocation sizes before anything runs; work items the
+// reference computes but never stores (attention and PLE-gate groups beyond
+// `heads` / `streams`) are skipped.
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cmath>
+#include <string>
+
+#include "internal.h"
+#include "strata_device.h"
+
+using namespace smi;
+
+namespace {
+
+constexpr float kNegBig = -3.402823e38f;  // the reference's initial maximum (kernels/strata.cu:337,388)
+
+// IQ4_NL codebook (kernels/strata.cu:22-31).
+__constant__ float kIq4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+__device__ __forceinline__ float iq4_value(int c) { return kIq4[c & 15]; }
+__device__ __forceinline__ int item() { return (int)(blockIdx.x * blockDim.x + threadIdx.x); }
+
+// kernels/strata.cu:72-80
+__global__ void k_embedding(const float *Values, const uint32_t *Codes, const float *Scales, const float *Offsets,
+                            float *Residual, int width, int streams, int outputOffset, int format, int bits,
+                            int groupSize, int bias, int codebook, int hasOffset, int n) {
+    int i = item();
+    if (i >= n) return;
+    float value = 0.0f;
+    if (format == 0) {
+        value = Values[i];
+    } else if (format == 1) {
+        value = __uint_as_float(((Codes[i / 2] >> ((i % 2) * 16)) & 65535u) << 16);
+    } else {
+        int bit = i * bits, group = i / groupSize;
+        int code = (int)((Codes[bit / 32] >> (bit % 32)) & ((1u << bits) - 1u));
+        value = (codebook == 1 ? iq4_value(code) : (float)(code + bias)) * Scales[group];
+        if (hasOffset != 0) value = value + Offsets[group];
+    }
+    for (int s = 0; s < streams; ++s) Residual[outputOffset + s * width + i] = value;
+}
+
+// kernels/strata.cu:90-104: ln(base) by the atanh series (25 odd terms) after
+// halving base below 2, the power split into whole multiples of ln 2 and a
+// remainder, 2^remainder-ish by a 20-term exp series, scaled by halvings.
+__global__ void k_rope_frequencies(float *High, float *Low, int rotary, float base, int n) {
+    int i = item();
+    if (i >= n) return;
+    const double ln2 = 0.693147180559945309417232121458176568;
+    double m = (double)base;
+    int ex = 0;
+    while (m >= 2.0) {
+        m = m * 0.5;
+        ex += 1;
+    }
+    double y = (m - 1.0) / (m + 1.0), term = y, lg = 0.0;
+    for (int k = 1; k <= 49; k += 2) {
+        lg = lg + term / (double)k;
+        term = term * y * y;
+    }
+    lg = 2.0 * lg + (double)ex * ln2;
+    double power = -lg * (double)(2 * i) / (double)rotary;
+    int whole = (int)(float)(power / ln2);
+    double rem = power - (double)whole * ln2, result = 1.0;
+    term = 1.0;
+    for (int k = 1; k <= 20; ++k) {
+        term = term * rem / (double)k;
+        result = result + term;
+    }
+    for (; whole < 0; whole++) result = result * 0.5;
+    High[i] = (float)result;
+    Low[i] = (float)(result - (double)High[i]);
+}
+
+// kernels/strata.cu:105-111
+__global__ void k_rope_table(const float *High, const float *Low, float *Cos, float *Sin, int half, int n) {
+    int i = item();
+    if (i >= n) return;
+    const double turn = 6.283185307179586476925286766559005768;
+    int pair = i % half;
+    double angle = (double)(i / half) * ((double)High[pair] + (double)Low[pair]);
+    int wraps = (int)(float)(angle / turn + 0.5);
+    float reduced = (float)(angle - (double)wraps * turn), s, c;
+    sm::sincos_or(reduced, s, c);
+    Cos[i] = c;
+    Sin[i] = s;
+}
+
+// kernels/strata.cu:113-120
+__global__ void k_rope_position(const float *X, const float *Cos, const float *Sin, float *Y, int dim, int heads,
+                                int rotary, int position, int n) {
+    int i = item();
+    if (i >= n) return;
+    int d = i % dim;
+    if (d >= rotary) {
+        Y[i] = X[i];
+        return;
+    }
+    int half = rotary / 2, pair = d % half, row = i - d;
+    int angle = (position + i / (dim * heads)) * half + pair;
+    float c = Cos[angle], s = Sin[angle], a = X[row + pair], b = X[row + pair + half];
+    Y[i] = d < half ? a * c - b * s : b * c + a * s;
+}
+
+// kernels/strata.cu:273-277
+__global__ void k_hc_mix(const float *Norm, const float *Gate, float *Mixed, int width, int streams, int n) {
+    int i = item();
+    if (i >= n) return;
+    float v = 0.0f;
+    for (int c = 0; c < streams; ++c) v = v + Norm[c * width + i] * sm::sigmoid(Gate[c * width + i]);
+    Mixed[i] = v / (float)streams;
+}
+// kernels/strata.cu:278-281
+__global__ void k_hc_write(float *Residual, const float *Output, const float *Inject, int width, int streams, int n) {
+    int i = item();
+    if (i >= n) return;
+    Residual[i] = Residual[i] + Output[i % width] * (2.0f * sm::sigmoid(Inject[i / width] / (float)streams));
+}
+
+// kernels/strata.cu:287-295: one channel per lane; the channel's history
+// shifts by one after the output is formed.
+__global__ void k_conv(float *History, const float *X, const float *W, float *Y, int taps, int dilation,
+                       int activation, int n) {
+    int c = item();
+    if (c >= n) return;
+    int span = (taps - 1) * dilation;
+    float *h = History + (int64_t)c * span;
+    float sum = 0.0f;
+    for (int t = 0; t < taps - 1; ++t) sum = sum + h[t * dilation] * W[c * taps + t];
+    sum = sum + X[c] * W[c * taps + taps - 1];
+    Y[c] = activation == 1 ? sm::silu(sum) : sum;
+    for (int t = 0; t < span - 1; ++t) h[t] = h[t + 1];
+    if (span > 0) h[span - 1] = X[c];
+}
+
+// kernels/strata.cu:296-302
+__global__ void k_gdn_gates(const float *Alpha, const float *Beta, const float *A, const float *Dt, float *Decay,
+                            float *Strength, int n) {
+    int h = item();
+    if (h >= n) return;
+    float a = Alpha[h] + Dt[h];
+    float sp = a > 20.0f ? a : sm::logf_or(1.0f + sm::expf_or(a));
+    Decay[h] = sm::expf_or(A[h] * sp);
+    Strength[h] = sm::sigmoid(Beta[h]);
+}
+
+// kernels/strata.cu:304-313: one (value head, value component) per lane;
+// state [key dim][value head][value dim], so lanes of one key index read
+// consecutive words.
+__global__ void k_gdn_step(float *State, const float *Q, const float *K, const float *V, const float *Decay,
+                           const float *Beta, float *Y, int dim, int keyHeads, int valueHeads, int n) {
+    int jh = item();
+    if (jh >= n) return;
+    int h = jh / dim, kh = h % keyHeads, stride = valueHeads * dim;
+    float decay = Decay[h], prediction = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+        int ix = i * stride + jh;
+        float s = State[ix] * decay;
+        State[ix] = s;
+        prediction = prediction + s * K[kh * dim + i];
+    }
+    float delta = (V[jh] - prediction) * Beta[h], result = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+        int ix = i * stride + jh;
+        float s = State[ix] + K[kh * dim + i] * delta;
+        State[ix] = s;
+        result = result + s * Q[kh * dim + i];
+    }
+    Y[jh] = result;
+}
+
+// kernels/strata.cu:314-316
+__global__ void k_slice(const float *X, float *Y, int width, int stride, int offset, int n) {
+    int i = item();
+    if (i < n) Y[i] = X[(i / width) * stride + offset + i % width];
+}
+// kernels/strata.cu:328-330
+__global__ void k_kv_append(const float *K, const float *V, float *Keys, float *Values, int width, int position,
+                            int n) {
+    int i = item();
+    if (i >= n) return;
+    Keys[position * width + i] = K[i];
+    Values[position * width + i] = V[i];
+}
+
+// kernels/strata.cu:334-356: one 64-lane block per (head, 64-component
+// tile). Lane-strided scores (sequential dot over the head dimension), the
+// reference's maximum tree, exponentials with the lane-strided sum and its
+// tree, then per component the sequential weighted sum over the cells.
+__global__ __launch_bounds__(64) void k_attention(const float *Q, const float *Keys, const float *Values,
+                                                  const int *Cells, float *Y, int dim, int heads, int kvHeads,
+                                                  int count, float scale) {
+    __shared__ float scores[2048];
+    const int lane = threadIdx.x, h = blockIdx.x, d = blockIdx.y * 64 + lane;
+    const int kh = h / (heads / kvHeads);
+    const float *q = Q + h * dim;
+    float mx = kNegBig;
+    for (int t = lane; t < count; t += 64) {
+        const float *k = Keys + (int64_t)(Cells[t] * kvHeads + kh) * dim;
+        float score = 0.0f;
+        for (int j = 0; j < dim; ++j) score = score + q[j] * k[j];
+        score = score * scale;
+        scores[t] = score;
+        mx = fmaxf(mx, score);
+    }
+    for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_down(mx, s, 64));
+    mx = __shfl(mx, 0, 64);
+    float sum = 0.0f;
+    for (int t = lane; t < count; t += 64) {
+        float p = sm::expf_or(scores[t] - mx);
+        scores[t] = p;
+        sum = sum + p;
+    }
+    float total = __shfl(sm::tree_sum64(sum), 0, 64);
+    __syncthreads();
+    if (d >= dim) return;
+    float value = 0.0f;
+    for (int t = 0; t < count; ++t) value = value + scores[t] * Values[(int64_t)(Cells[t] * kvHeads + kh) * dim + d];
+    Y[h * dim + d] = value / total;
+}
+
+// kernels/strata.cu:357-359
+__global__ void k_attention_gate(const float *Attention, const float *FullQ, float *Y, int dim, int n) {
+    int i = item();
+    if (i < n) Y[i] = Attention[i] * sm::sigmoid(FullQ[(i / dim) * dim * 2 + dim + i % dim]);
+}
+
+// kernels/strata.cu:367-377: one 64-lane block per stream.
+__global__ __launch_bounds__(64) void k_ple_gate(const float *Key, const float *Query, float *Gate, int width) {
+    const int lane = threadIdx.x, c = blockIdx.x;
+    float dot = 0.0f;
+    for (int d = lane; d < width; d += 64) dot = dot + Key[c * width + d] * Query[c * width + d];
+    dot = sm::tree_sum64(dot);
+    if (lane != 0) return;
+    float v = dot / sqrtf((float)width);
+    float sign = v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f);
+    Gate[c] = sm::sigmoid(sign * sqrtf(fmaxf(fabsf(v), 0.000001f)));
+}
+// kernels/strata.cu:378-380
+__global__ void k_ple_broadcast(const float *Value, const float *Gate, float *Y, int width, int n) {
+    int i = item();
+    if (i < n) Y[i] = Value[i % width] * Gate[i / width];
+}
+// kernels/strata.cu:381-383
+__global__ void k_ple_add(float *Residual, const float *Gated, const float *Conv, int n) {
+    int i = item();
+    if (i < n) Residual[i] = Residual[i] + (Gated[i] + Conv[i]);
+}
+
+// kernels/strata.cu:386-396: lane-strided best (lowest index on ties), then
+// the reference's tree with the same rule.
+__global__ __launch_bounds__(64) void k_argmax(const float *Logits, int *Token, int count) {
+    const int lane = threadIdx.x;
+    float best = kNegBig;
+    int id = count;
+    for (int i = lane; i < count; i += 64) {
+        float v = Logits[i];
+        if (v > best || (v == best && i < id)) {
+            best = v;
+            id = i;
+        }
+    }
+    for (int s = 32; s > 0; s >>= 1) {
+        float ov = __shfl_down(best, s, 64);
+        int oi = __shfl_down(id, s, 64);
+        if (lane < s && (ov > best || (ov == best && oi < id))) {
+            best = ov;
+            id = oi;
+        }
+    }
+    if (lane == 0) Token[0] = id;
+}
+
+// ------------------------------------------------------------- launchers
+int bad(sm_ctx *ctx, const std::string &m) { return fail(ctx, SM_E_ARG, m); }
+unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
+// Items a 64-lane grid of G[0] workgroups covers.
+int64_t covered(const uint32_t *G, int64_t n) { return std::min<int64_t>(n, (int64_t)G[0] * 64); }
+const float *F(Args a, int i) { return (const float *)a.ptr(i); }
+float *Fw(Args a, int i) { return (float *)a.ptr(i); }
+
+int L_embedding(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(5), streams = a.i32(6), off = a.i32(7), format = a.i32(8), bits = a.i32(9), group = a.i32(10);
+    int bias = a.i32(11), codebook = a.i32(12), hasOffset = a.i32(13);
+    if (width < 1 || streams < 1) return bad(ctx, "strata_embedding: width and streams must be >= 1");
+    if (off < 0) return bad(ctx, "embedding output offset must be >= 0");
+    int64_t rlen = buf_len(ctx, a.ptr(4));
+    if (format < 0 || format > 2 || (rlen >= 0 && off + (int64_t)width * streams > rlen / 4))
+        return fail(ctx, SM_E_ARG, "Embedding exceeds buffer layout");
+    if (format == 2 && ((bits != 2 && bits != 4 && bits != 8) || group < 1 || width % group))
+        return fail(ctx, SM_E_ARG, "Invalid packed embedding layout");
+    int64_t n = covered(G, width);
+    if (int rc = need(ctx, a.ptr(4), (uint64_t)(off + (int64_t)(streams - 1) * width + n) * 4, "Residual")) return rc;
+    if (format == 0) {
+        if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "Values")) return rc;
+    } else if (format == 1) {
+        if (int rc = need(ctx, a.ptr(1), (uint64_t)(n + 1) / 2 * 4, "Codes")) return rc;
+    } else {
+        if (int rc = need(ctx, a.ptr(1), (uint64_t)(n * bits + 31) / 32 * 4, "Codes")) return rc;
+        uint64_t groups = (uint64_t)((n - 1) / group + 1);
+        if (int rc = need(ctx, a.ptr(2), groups * 4, "Scales")) return rc;
+        if (hasOffset)
+            if (int rc = need(ctx, a.ptr(3), groups * 4, "Offsets")) return rc;
+    }
+    k_embedding<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), (const uint32_t *)a.ptr(1), F(a, 2), F(a, 3), Fw(a, 4),
+                                                       width, streams, off, format, bits, group, bias, codebook,
+                                                       hasOffset, (int)n);
+    return launched(ctx);
+}
+
+int L_rope_frequencies(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int rotary = a.i32(2);
+    float base = a.f32(3);
+    if (!std::isfinite(base) || base <= 1.0f || rotary < 1 || rotary % 2)
+        return fail(ctx, SM_E_ARG, "Invalid RoPE frequencies");
+    int64_t n = covered(G, rotary / 2);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "High")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "Low")) return rc;
+    k_rope_frequencies<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), Fw(a, 1), rotary, base, (int)n);
+    return launched(ctx);
+}
+
+int L_rope_table(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int rotary = a.i32(4), context = a.i32(5);
+    if (rotary < 2 || rotary % 2 || context < 1) return bad(ctx, "strata_rope_table: rotary >= 2 even, context >= 1");
+    int half = rotary / 2;
+    int64_t n = covered(G, (int64_t)context * half);
+    uint64_t pairs = (uint64_t)std::min<int64_t>(n, half);
+    if (int rc = need(ctx, a.ptr(0), pairs * 4, "High")) return rc;
+    if (int rc = need(ctx, a.ptr(1), pairs * 4, "Low")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Cos")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)n * 4, "Sin")) return rc;
+    k_rope_table<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), Fw(a, 3), half, (int)n);
+    return launched(ctx);
+}
+
+int L_rope_position(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(4), heads = a.i32(5), rotary = a.i32(6), position = a.i32(7), tokens = a.i32(8);
+    if (position < 0 || position > 2047) return bad(ctx, "RoPE position must be an integer in [0, 2047]");
+    if (dim < 1 || heads < 1 || rotary < 1 || tokens < 1)
+        return bad(ctx, "strata_rope_position: dim, heads, rotary, tokens must be >= 1");
+    int64_t xlen = buf_len(ctx, a.ptr(0)), clen = buf_len(ctx, a.ptr(1)), slen = buf_len(ctx, a.ptr(2)),
+            ylen = buf_len(ctx, a.ptr(3)), total = (int64_t)dim * heads * tokens;
+    if (rotary % 2 || rotary > dim || position + tokens > 2048 || clen < (int64_t)(position + tokens) * rotary / 2 * 4 ||
+        slen != clen || xlen != total * 4 || ylen != xlen)
+        return fail(ctx, SM_E_ARG, "Invalid RoPE layout");
+    int64_t n = covered(G, total);
+    k_rope_position<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3), dim, heads, rotary,
+                                                           position, (int)n);
+    return launched(ctx);
+}
+
+int L_hc_mix(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4);
+    if (width < 1 || streams < 1) return bad(ctx, "strata_hc_mix: width and streams must be >= 1");
+    int64_t n = covered(G, width);
+    uint64_t span = (uint64_t)((int64_t)(streams - 1) * width + n) * 4;
+    if (int rc = need(ctx, a.ptr(0), span, "Norm")) return rc;
+    if (int rc = need(ctx, a.ptr(1), span, "Gate")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Mixed")) return rc;
+    k_hc_mix<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), width, streams, (int)n);
+    return launched(ctx);
+}
+
+int L_hc_write(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4);
+    if (width < 1 || streams < 1) return bad(ctx, "strata_hc_write: width and streams must be >= 1");
+    int64_t n = covered(G, (int64_t)width * streams);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "Residual")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)std::min<int64_t>(n, width) * 4, "Output")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)((n - 1) / width + 1) * 4, "Inject")) return rc;
+    k_hc_write<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), width, streams, (int)n);
+    return launched(ctx);
+}
+
+int L_conv(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int channels = a.i32(4), taps = a.i32(5), dilation = a.i32(6), activation = a.i32(7);
+    if (channels < 1 || taps < 1 || dilation < 1)
+        return bad(ctx, "strata_conv: channels, taps and dilation must be >= 1");
+    int64_t n = covered(G, channels), span = (int64_t)(taps - 1) * dilation;
+    if (span > 0)
+        if (int rc = need(ctx, a.ptr(0), (uint64_t)(n * span) * 4, "History")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "X")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)(n * taps) * 4, "W")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)n * 4, "Y")) return rc;
+    k_conv<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), Fw(a, 3), taps, dilation, activation,
+                                                  (int)n);
+    return launched(ctx);
+}
+
+int L_gdn_gates(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int heads = a.i32(6);
+    if (heads < 1) return bad(ctx, "strata_gdn_gates: heads must be >= 1");
+    int64_t n = covered(G, heads);
+    const char *names[6] = {"Alpha", "Beta", "A", "Dt", "Decay", "Strength"};
+    for (int i = 0; i < 6; i++)
+        if (int rc = need(ctx, a.ptr(i), (uint64_t)n * 4, names[i])) return rc;
+    k_gdn_gates<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), F(a, 3), Fw(a, 4), Fw(a, 5),
+                                                       (int)n);
+    return launched(ctx);
+}
+
+int L_gdn_step(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(7), keyHeads = a.i32(8), valueHeads = a.i32(9);
+    if (dim < 1 || keyHeads < 1 || valueHeads < 1)
+        return bad(ctx, "strata_gdn_step: dim, keyHeads, valueHeads must be >= 1");
+    int64_t n = covered(G, (int64_t)dim * valueHeads), heads = (n - 1) / dim + 1;
+    int64_t keyRows = std::min<int64_t>(keyHeads, heads);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)((int64_t)(dim - 1) * valueHeads * dim + n) * 4, "State")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)(keyRows * dim) * 4, "Q")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)(keyRows * dim) * 4, "K")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)n * 4, "V")) return rc;
+    if (int rc = need(ctx, a.ptr(4), (uint64_t)heads * 4, "Decay")) return rc;
+    if (int rc = need(ctx, a.ptr(5), (uint64_t)heads * 4, "Beta")) return rc;
+    if (int rc = need(ctx, a.ptr(6), (uint64_t)n * 4, "Y")) return rc;
+    k_gdn_step<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), F(a, 3), F(a, 4), F(a, 5), Fw(a, 6),
+                                                      dim, keyHeads, valueHeads, (int)n);
+    return launched(ctx);
+}
+
+int L_slice(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(2), rows = a.i32(3), stride = a.i32(4), offset = a.i32(5);
+    if (width < 1 || rows < 1) return bad(ctx, "slice width and rows must be >= 1");
+    if (stride < 0 || offset < 0) return bad(ctx, "strata_slice: stride and offset must be >= 0");
+    int64_t n = covered(G, (int64_t)width * rows), last = n - 1;
+    // Largest source index: the last item, or the end of the row before it.
+    int64_t top = (last / width) * stride + offset + last % width;
+    if (last >= width) top = std::max<int64_t>(top, (last / width - 1) * stride + offset + width - 1);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)(top + 1) * 4, "X")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "Y")) return rc;
+    k_slice<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), Fw(a, 1), width, stride, offset, (int)n);
+    return launched(ctx);
+}
+
+int L_kv_append(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(4), position = a.i32(5);
+    if (width < 1 || position < 0) return bad(ctx, "strata_kv_append: width >= 1 and position >= 0");
+    int64_t n = covered(G, width);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "K")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "V")) return rc;
+    uint64_t end = (uint64_t)((int64_t)position * width + n) * 4;
+    if (int rc = need(ctx, a.ptr(2), end, "Keys")) return rc;
+    if (int rc = need(ctx, a.ptr(3), end, "Values")) return rc;
+    k_kv_append<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), Fw(a, 3), width, position, (int)n);
+    return launched(ctx);
+}
+
+int L_attention(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(5), heads = a.i32(6), kvHeads = a.i32(7), count = a.i32(8);
+    float scale = a.f32(9);
+    if (dim < 1 || heads < 1 || kvHeads < 1) return bad(ctx, "strata_attention: dim, heads, kvHeads must be >= 1");
+    if (heads % kvHeads) return bad(ctx, "Attention heads must be divisible by KV heads");
+    if (count < 1 || count > 2048) return bad(ctx, "attention selected cells must be an integer in [1, 2048]");
+    int hu = (int)std::min<int64_t>(G[0], heads), tiles = (int)std::min<int64_t>(G[1], (dim + 63) / 64);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)hu * dim * 4, "Q")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)count * 4, "Cells")) return rc;
+    int64_t written = (int64_t)(hu - 1) * dim + std::min<int64_t>(dim, (int64_t)tiles * 64);
+    if (int rc = need(ctx, a.ptr(4), (uint64_t)written * 4, "Y")) return rc;
+    // Cells index rows of kvHeads * dim values in Keys and Values.
+    int64_t klen = buf_len(ctx, a.ptr(1)), vlen = buf_len(ctx, a.ptr(2));
+    if (klen < 0) return need(ctx, a.ptr(1), 0, "Keys");
+    if (vlen < 0) return need(ctx, a.ptr(2), 0, "Values");
+    int64_t rowsAvail = std::min(klen, vlen) / 4 / ((int64_t)kvHeads * dim);
+    if (int rc = check_indices(ctx, a.ptr(3), count, 1, 0, 0, (int)std::min<int64_t>(rowsAvail, 0x7fffffff),
+                               "Attention cells"))
+        return rc;
+    k_attention<<<dim3(hu, tiles), 64, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), (const int *)a.ptr(3), Fw(a, 4),
+                                                          dim, heads, kvHeads, count, scale);
+    return launched(ctx);
+}
+
+int L_attention_gate(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(3), heads = a.i32(4);
+    if (dim < 1 || heads < 1) return bad(ctx, "strata_attention_gate: dim and heads must be >= 1");
+    int64_t n = covered(G, (int64_t)dim * heads), last = n - 1;
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "Attention")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)((last / dim) * dim * 2 + dim + last % dim + 1) * 4, "FullQ"))
+        return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Y")) return rc;
+    k_attention_gate<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), dim, (int)n);
+    return launched(ctx);
+}
+
+int L_ple_gate(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4);
+    if (width < 1 || streams < 1) return bad(ctx, "strata_ple_gate: width and streams must be >= 1");
+    int cu = (int)std::min<int64_t>(G[0], streams);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)cu * width * 4, "Key")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)cu * width * 4, "Query")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)cu * 4, "Gate")) return rc;
+    k_ple_gate<<<cu, 64, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), width);
+    return launched(ctx);
+}
+
+int L_ple_broadcast(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4);
+    if (width < 1 || streams < 1) return bad(ctx, "strata_ple_broadcast: width and streams must be >= 1");
+    int64_t n = covered(G, (int64_t)width * streams);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)std::min<int64_t>(n, width) * 4, "Value")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)((n - 1) / width + 1) * 4, "Gate")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Y")) return rc;
+    k_ple_broadcast<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), width, (int)n);
+    return launched(ctx);
+}
+
+int L_ple_add(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int count = a.i32(3);
+    if (count < 0) return bad(ctx, "strata_ple_add: n must be >= 0");
+    int64_t n = covered(G, count);
+    if (n == 0) return SM_OK;
+    const char *names[3] = {"Residual", "Gated", "Conv"};
+    for (int i = 0; i < 3; i++)
+        if (int rc = need(ctx, a.ptr(i), (uint64_t)n * 4, names[i])) return rc;
+    k_ple_add<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), (int)n);
+    return launched(ctx);
+}
+
+int L_argmax(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int count = a.i32(2);
+    if (count < 0) return bad(ctx, "strata_argmax: count must be >= 0");
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)count * 4, "Logits")) return rc;
+    if (int rc = need(ctx, a.ptr(1), 4, "Token")) return rc;
+    // Every workgroup of the reference computes the same winner; one suffices.
+    k_argmax<<<1, 64, 0, ctx->stream>>>(F(a, 0), (int *)a.ptr(1), count);
+    return launched(ctx);
+}
+
+// Parameter lists in the reference's order (kernels/strata.cu).
+const Entry kModelEntries[] = {
+    {"strata_embedding",
+     "Values:f32*,Codes:u32*,Scales:f32*,Offsets:f32*,Residual:f32*,width:i32,streams:i32,outputOffset:i32,format:i32,"
+     "bits:i32,groupSize:i32,bias:i32,codebook:i32,hasOffset:i32",
+     14, L_embedding},
+    {"strata_rope_frequencies", "High:f32*,Low:f32*,rotary:i32,base:f32", 4, L_rope_frequencies},
+    {"strata_rope_table", "High:f32*,Low:f32*,Cos:f32*,Sin:f32*,rotary:i32,context:i32", 6, L_rope_table},
+    {"strata_rope_position", "X:f32*,Cos:f32*,Sin:f32*,Y:f32*,dim:i32,heads:i32,rotary:i32,position:i32,tokens:i32", 9,
+     L_rope_position},
+    {"strata_hc_mix", "Norm:f32*,Gate:f32*,Mixed:f32*,width:i32,streams:i32", 5, L_hc_mix},
+    {"strata_hc_write", "Residual:f32*,Output:f32*,Inject:f32*,width:i32,streams:i32", 5, L_hc_write},
+    {"strata_conv", "History:f32*,X:f32*,W:f32*,Y:f32*,channels:i32,taps:i32,dilation:i32,activation:i32", 8, L_conv},
+    {"strata_gdn_gates", "Alpha:f32*,Beta:f32*,A:f32*,Dt:f32*,Decay:f32*,Strength:f32*,heads:i32", 7, L_gdn_gates},
+    {"strata_gdn_step",
+     "State:f32*,Q:f32*,K:f32*,V:f32*,Decay:f32*,Beta:f32*,Y:f32*,dim:i32,keyHeads:i32,valueHeads:i32", 10,
+     L_gdn_step},
+    {"strata_slice", "X:f32*,Y:f32*,width:i32,rows:i32,stride:i32,offset:i32", 6, L_slice},
+    {"strata_kv_append", "K:f32*,V:f32*,Keys:f32*,Values:f32*,width:i32,position:i32", 6, L_kv_append},
+    {"strata_attention",
+     "Q:f32*,Keys:f32*,Values:f32*,Cells:i32*,Y:f32*,dim:i32,heads:i32,kvHeads:i32,count:i32,scale:f32", 10,
+     L_attention},
+    {"strata_attention_gate", "Attention:f32*,FullQ:f32*,Y:f32*,dim:i32,heads:i32", 5, L_attention_gate},
+    {"strata_ple_gate", "Key:f32*,Query:f32*,Gate:f32*,width:i32,streams:i32", 5, L_ple_gate},
+    {"strata_ple_broadcast", "Value:f32*,Gate:f32*,Y:f32*,width:i32,streams:i32", 5, L_ple_broadcast},
+    {"strata_ple_add", "Residual:f32*,Gated:f32*,Conv:f32*,n:i32", 4, L_ple_add},
+    {"strata_argmax", "Logits:f32*,Token:i32*,count:i32", 3, L_argmax},
+};
+
+}  // namespace
+
+namespace smi {
+const Entry *model_entries(int *count) {
+    *count = (int)(sizeof(kModelEntries) / sizeof(kModelEntries[0]));
+    return kModelEntries;
+}
+}  // namespace smi

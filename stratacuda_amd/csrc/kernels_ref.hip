@@ -252,27 +252,16 @@ __global__ void k_check_indices(const int *idx, int64_t n, int64_t stride, int64
     if (v < lo || v >= hi) atomicOr(bad, 1u);
 }
 
-// ---------------------------------------------------------- host side
-struct Args {
-    const uint64_t *a;
-    uint64_t ptr(int i) const { return a[i]; }
-    int i32(int i) const { return (int)(uint32_t)(a[i] & 0xffffffffu); }
-    float f32(int i) const {
-        uint32_t u = (uint32_t)(a[i] & 0xffffffffu);
-        float f;
-        memcpy(&f, &u, 4);
-        return f;
-    }
-};
+}  // namespace
 
-int bad(sm_ctx *ctx, const std::string &m) { return fail(ctx, SM_E_ARG, m); }
+namespace smi {
 
 int64_t buf_len(sm_ctx *ctx, uint64_t h) {
     auto it = ctx->buffers.find(h);
     return it == ctx->buffers.end() ? -1 : (int64_t)it->second;
 }
 
-// Device-side index validation for Mapping / Indices buffers.
+// Device-side index validation for Mapping / Indices / Cells buffers.
 int check_indices(sm_ctx *ctx, uint64_t buf, int64_t n, int64_t stride, int64_t first, int lo, int hi,
                   const char *what) {
     if (n <= 0) return SM_OK;
@@ -290,6 +279,13 @@ int check_indices(sm_ctx *ctx, uint64_t buf, int64_t n, int64_t stride, int64_t 
     if (flag) return fail(ctx, SM_E_BOUNDS, std::string(what) + ": an index points outside the buffer layout");
     return SM_OK;
 }
+
+}  // namespace smi
+
+namespace {
+
+// ---------------------------------------------------------- host side
+int bad(sm_ctx *ctx, const std::string &m) { return fail(ctx, SM_E_ARG, m); }
 
 unsigned blocks_for(uint64_t logical) { return (unsigned)((logical + kGroupsPerBlock - 1) / kGroupsPerBlock); }
 
@@ -550,14 +546,6 @@ int rows_common(sm_ctx *ctx, const uint32_t *G, Args a, bool scatter) {
 int L_gather_rows(sm_ctx *ctx, const uint32_t *G, Args a) { return rows_common(ctx, G, a, false); }
 int L_scatter_rows(sm_ctx *ctx, const uint32_t *G, Args a) { return rows_common(ctx, G, a, true); }
 
-typedef int (*Launcher)(sm_ctx *, const uint32_t *, Args);
-struct Entry {
-    const char *name;
-    const char *signature;
-    int nargs;
-    Launcher launch;
-};
-
 // Parameter lists in the reference's order (kernels/strata.cu).
 const Entry kEntries[] = {
     {"strata_unpack_half", "Packed:u32*,Values:f32*,count:i32", 3, L_unpack_half},
@@ -595,10 +583,23 @@ const Entry kEntries[] = {
 };
 const int kEntryCount = sizeof(kEntries) / sizeof(kEntries[0]);
 
+// The MoE path's kernels (this file) first, then the fixture model's.
+const Entry *entry_at(int index) {
+    int model_count = 0;
+    const Entry *model = model_entries(&model_count);
+    if (index >= 0 && index < kEntryCount) return &kEntries[index];
+    if (index >= kEntryCount && index < kEntryCount + model_count) return &model[index - kEntryCount];
+    return nullptr;
+}
+int entry_count() {
+    int model_count = 0;
+    model_entries(&model_count);
+    return kEntryCount + model_count;
+}
 const Entry *find_entry(const char *name) {
     if (!name) return nullptr;
-    for (int i = 0; i < kEntryCount; i++)
-        if (!strcmp(kEntries[i].name, name)) return &kEntries[i];
+    for (int i = 0, n = entry_count(); i < n; i++)
+        if (!strcmp(entry_at(i)->name, name)) return entry_at(i);
     return nullptr;
 }
 
@@ -616,8 +617,11 @@ int norm_launch(sm_ctx *ctx, const float *X, const float *gamma, float *Y, int c
 
 extern "C" {
 
-int sm_kernel_count(void) { return kEntryCount; }
-const char *sm_kernel_name(int index) { return index >= 0 && index < kEntryCount ? kEntries[index].name : nullptr; }
+int sm_kernel_count(void) { return entry_count(); }
+const char *sm_kernel_name(int index) {
+    const Entry *e = entry_at(index);
+    return e ? e->name : nullptr;
+}
 const char *sm_kernel_signature(const char *name) {
     const Entry *e = find_entry(name);
     return e ? e->signature : nullptr;

@@ -95,6 +95,67 @@ __device__ __forceinline__ float sigmoid(float x, const uint64_t *tab = kExp2Tab
 }
 __device__ __forceinline__ float silu(float x, const uint64_t *tab = kExp2Tab) { return x * sigmoid(x, tab); }
 
+// ------------------------------------------------------ logf, sin, cos
+// Evaluated in double arithmetic (every operation rounded separately) and
+// rounded once to float; the CPU oracle evaluates the same operations, so
+// both produce the same bits. Within one ulp of libm over the ranges used.
+//
+// ln x: x = m 2^e, m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(y) with
+// y = (m-1)/(m+1) by the odd series to y^27 (Horner in y^2).
+__device__ inline float logf_or(float x) {
+    if (x != x) return x;
+    if (x < 0.0f) return __uint_as_float(0x7fc00000u);
+    if (x == 0.0f) return __uint_as_float(0xff800000u);
+    if (x == __uint_as_float(0x7f800000u)) return x;
+    uint64_t u = (uint64_t)__double_as_longlong((double)x);
+    int e = (int)((u >> 52) & 2047u) - 1023;
+    double m = __longlong_as_double((long long)((u & 0x000fffffffffffffull) | 0x3ff0000000000000ull));
+    if (m >= 1.4142135623730951) {
+        m = m * 0.5;
+        e = e + 1;
+    }
+    double y = (m - 1.0) / (m + 1.0), y2 = y * y, p = 1.0 / 27.0;
+#pragma unroll
+    for (int n = 25; n >= 1; n -= 2) p = p * y2 + 1.0 / (double)n;
+    return (float)(2.0 * (y * p) + (double)e * 0.6931471805599453);
+}
+// sin and cos of |r| <= 4: r = k pi/2 + t, |t| <= pi/4 (pi/2 as a 33-bit
+// head plus a tail), Taylor series of sin t to t^19 and cos t to t^20.
+__device__ inline void sincos_or(float r, float &s_out, float &c_out) {
+    const double PIO2_HI = 1.57079632673412561417e+00, PIO2_LO = 6.07710050650619224932e-11;
+    double x = (double)r;
+    double kd = x * 0.63661977236758134308;
+    int k = (int)(kd >= 0.0 ? kd + 0.5 : kd - 0.5);
+    double t = (x - (double)k * PIO2_HI) - (double)k * PIO2_LO, t2 = t * t;
+    double as[10], ac[11], fs = 1.0, fc = 1.0, sn = 0.0, cs = 0.0;
+    as[0] = 1.0;
+    ac[0] = 1.0;
+#pragma unroll
+    for (int j = 1; j < 10; j++) {
+        fs = fs / (double)(2 * j) / (double)(2 * j + 1);
+        as[j] = fs;
+    }
+#pragma unroll
+    for (int j = 1; j < 11; j++) {
+        fc = fc / (double)(2 * j - 1) / (double)(2 * j);
+        ac[j] = fc;
+    }
+#pragma unroll
+    for (int j = 9; j >= 0; j--) sn = sn * (-t2) + as[j];
+#pragma unroll
+    for (int j = 10; j >= 0; j--) cs = cs * (-t2) + ac[j];
+    sn = sn * t;
+    double s, c;
+    switch (k & 3) {
+    case 0: s = sn; c = cs; break;
+    case 1: s = cs; c = -sn; break;
+    case 2: s = -sn; c = -cs; break;
+    default: s = -cs; c = sn; break;
+    }
+    s_out = (float)s;
+    c_out = (float)c;
+}
+
 // --------------------------------------------------------- wave reductions
 // Cross-lane moves use DPP where the pattern allows: a DPP move costs a few
 // cycles, while a ds_bpermute shuffle (__shfl*) costs ~55 ns of latency on

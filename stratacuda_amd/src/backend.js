@@ -32,7 +32,8 @@ export function requireInteger(n, label, min = 1, max = 0x7fffffff) {
 }
 
 // Argument checks run before any launch, with the reference's conditions and
-// messages (src/backend.js:10-56) for the kernels this library provides.
+// messages (src/backend.js:10-56) for the kernels this library provides
+// (strata_ple_decode and the batched prompt kernels are not among them).
 const PROJECTIONS = ['strata_project', 'strata_quant_project', 'strata_bf16_project', 'strata_q2_project'];
 export function validateDispatch(name, args) {
     const get = k => requireInteger(args[k], name + '.' + k);
@@ -63,6 +64,27 @@ export function validateDispatch(name, args) {
         if (args.Hidden.length < tokens * args.ff || (args.mapped && args.Mapping.length < tokens * 2))
             throw Error('Packed expert batch exceeds buffer layout');
         if (name === 'strata_q2_down') requireInteger(args.outputOffset, 'expert output offset', 0);
+    }
+    if (name === 'strata_embedding') {
+        const count = get('width') * get('streams');
+        requireInteger(args.outputOffset, 'embedding output offset', 0);
+        if (args.outputOffset + count > args.Residual.length || [0, 1, 2].indexOf(args.format) < 0)
+            throw Error('Embedding exceeds buffer layout');
+        if (args.format === 2 && ([2, 4, 8].indexOf(args.bits) < 0 || args.width % get('groupSize')))
+            throw Error('Invalid packed embedding layout');
+    }
+    if (name === 'strata_rope_position') {
+        requireInteger(args.position, 'RoPE position', 0, 2047);
+        if (get('rotary') % 2 || args.rotary > get('dim') || args.position + get('tokens') > 2048 ||
+            args.Cos.length < (args.position + args.tokens) * args.rotary / 2 || args.Sin.length !== args.Cos.length ||
+            args.X.length !== args.dim * get('heads') * args.tokens || args.Y.length !== args.X.length)
+            throw Error('Invalid RoPE layout');
+    }
+    if (name === 'strata_rope_frequencies' && (!Number.isFinite(args.base) || args.base <= 1 || get('rotary') % 2))
+        throw Error('Invalid RoPE frequencies');
+    if (name === 'strata_attention') {
+        if (get('heads') % get('kvHeads')) throw new RangeError('Attention heads must be divisible by KV heads');
+        requireInteger(args.count, 'attention selected cells', 1, 2048);
     }
     if (name === 'strata_norm' && get('rows') % get('weightRows'))
         throw new RangeError('Normalization weight rows must divide input rows');

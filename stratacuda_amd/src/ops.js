@@ -1,7 +1,7 @@
 // Ops: kernel orchestration for the MoE path with the reference's op
 // signatures (src/ops.js:5-127: alloc / release / clearTemporary / mat /
-// vector / norm / elem / packedExpert / dispose), over a backend with the
-// reference interface (HipBackend here). Weights come from the resident
+// vector / norm / elem / packedExpert / embedding / ple / rotate / slice /
+// dispose), over a backend with the reference interface (HipBackend here). Weights come from the resident
 // WeightResidency; there is no streaming tile cache (everything is resident).
 // moe() is the fused stage for kind 'hip': one sm_moe_layer call per layer.
 import {requireInteger} from './backend.js';
@@ -11,7 +11,7 @@ export const grid = n => [Math.ceil(n / 64), 1, 1];
 export class Ops {
     constructor(backend, store) {
         this.b = backend; this.store = store; this.residency = null;
-        this.temporary = new Set(); this.dummy = null; this.workspace = null;
+        this.temporary = new Set(); this.dummy = null; this.workspace = null; this.rope = null;
     }
     // Temporaries are completely written by their producing kernel (src/ops.js:13-16).
     async alloc(dataOrLength, type) {
@@ -77,6 +77,51 @@ export class Ops {
         if (o.mapping) await this.release(map);
         return result;
     }
+    // embedding(token, output, outputOffset) (src/ops.js:73-78): row `token`
+    // of the resident f32 embedding, replicated over the HC streams.
+    async embedding(token, output, outputOffset) {
+        const g = this.store.config, table = this.residency.tensor('token_embd.weight');
+        requireInteger(token, 'token', 0, table.length / g.width - 1);
+        if (this.dummy === null) this.dummy = this.b.alloc(new Int32Array(1), 'i32');
+        const row = await this.alloc(g.width);
+        this.b.copy(table, row, g.width, token * g.width, 0);
+        await this.b.run('strata_embedding', {Values: row, Codes: this.dummy, Scales: this.dummy, Offsets: this.dummy,
+            Residual: output, width: g.width, streams: g.streams, outputOffset: outputOffset || 0, format: 0, bits: 0,
+            groupSize: 1, bias: 0, codebook: 0, hasOffset: 0}, grid(g.width));
+        await this.release(row);
+    }
+    // ple(token, previous) (src/ops.js:79-83): the f32 PLE rows of an
+    // in-memory store, gathered on the host by the n-gram hash.
+    async ple(token, previous) { return this.alloc(await this.store.pleRows(token, previous)); }
+    // rotate(x, heads, position, tokens) (src/ops.js:84-94): RoPE tables made
+    // once on the device (strata_rope_frequencies, strata_rope_table), then
+    // strata_rope_position.
+    async rotate(x, heads, position, tokens) {
+        tokens = tokens || 1;
+        const g = this.store.config, y = await this.alloc(x.length);
+        if (!this.rope) {
+            const rope = {cos: this.b.alloc(g.context * g.rotary / 2), sin: this.b.alloc(g.context * g.rotary / 2)};
+            const hi = await this.alloc(g.rotary / 2), lo = await this.alloc(g.rotary / 2);
+            await this.b.run('strata_rope_frequencies', {High: hi, Low: lo, rotary: g.rotary, base: g.ropeBase},
+                grid(g.rotary / 2));
+            await this.b.run('strata_rope_table', {High: hi, Low: lo, Cos: rope.cos, Sin: rope.sin, rotary: g.rotary,
+                context: g.context}, grid(g.context * g.rotary / 2));
+            await this.release(hi, lo);
+            this.rope = rope;
+        }
+        await this.b.run('strata_rope_position', {X: x, Cos: this.rope.cos, Sin: this.rope.sin, Y: y, dim: g.headDim,
+            heads, rotary: g.rotary, position, tokens}, grid(x.length));
+        return y;
+    }
+    // slice(x, width, rows, stride, offset) (src/ops.js:122-126).
+    async slice(x, width, rows, stride, offset) {
+        rows = rows === undefined ? 1 : rows; stride = stride === undefined ? width : stride; offset = offset || 0;
+        requireInteger(width, 'slice width'); requireInteger(rows, 'slice rows');
+        if (offset < 0 || (rows - 1) * stride + offset + width > x.length) throw Error('Slice exceeds buffer');
+        const y = await this.alloc(width * rows);
+        await this.b.run('strata_slice', {X: x, Y: y, width, rows, stride, offset}, grid(width * rows));
+        return y;
+    }
     // The fused MoE stage (kind 'hip'): y, plus the routed ids and weights
     // [tokens x topK] in the reference's selection order.
     async moe(layer, x, tokens, options) {
@@ -117,6 +162,7 @@ export class Ops {
     async dispose() {
         await this.clearTemporary();
         if (this.residency) await this.residency.dispose();
+        if (this.rope) { this.b.free(this.rope.cos); this.b.free(this.rope.sin); this.rope = null; }
         if (this.dummy) this.b.free(this.dummy);
         if (this.workspace) this.b.free(this.workspace);
         this.dummy = null; this.workspace = null;

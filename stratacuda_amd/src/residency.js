@@ -89,3 +89,52 @@ export class WeightResidency {
         this.layers.clear(); this.expertUsed = 0; this.denseUsed = 0;
     }
 }
+
+// The all-resident policy for a whole-model f32 store (the fixture's
+// MemoryStore): every tensor is uploaded once when the engine initialises and
+// stays in HBM until dispose, experts included, so nothing is streamed or
+// evicted. get / vector / hasExpert / admit / note / info as above.
+export class ModelResidency {
+    constructor(ops) {
+        this.ops = ops; this.b = ops.b; this.store = ops.store;
+        this.tensors = new Map(); this.frequency = new Map();
+        this.hits = 0; this.misses = 0; this.evictions = 0; this.denseUsed = 0; this.expertUsed = 0;
+        ops.residency = this;
+    }
+    async loadAll() {
+        for (const [name, t] of this.store.tensors) {
+            if (this.tensors.has(name)) continue;
+            if (t.format !== 'f32') throw Error('Resident model tensors must be F32: ' + name);
+            this.tensors.set(name, this.b.alloc(t.data, 'f32'));
+            if (expertKey(name)) this.expertUsed += t.data.byteLength; else this.denseUsed += t.data.byteLength;
+            this.misses++;
+        }
+    }
+    tensor(name) {
+        const buffer = this.tensors.get(name);
+        if (!buffer) throw Error(name + ' is not resident');
+        this.hits++;
+        return buffer;
+    }
+    // Whole tensors only: Ops.mat asks for every row of a projection.
+    async get(name, start, rows) {
+        const t = this.store.describe(name);
+        if (start !== 0 || rows !== product(t.shape) / t.shape[0]) return null;
+        const data = this.tensor(name);
+        return {format: 'f32', data, buffers: [], bytes: data.byteLength};
+    }
+    async vector(name) { return this.tensor(name); }
+    hasExpert(key) { return true; }
+    note(key, count) { this.frequency.set(key, (this.frequency.get(key) || 0) + (count === undefined ? 1 : count)); }
+    async admit(key) { this.hits++; return true; }
+    info() {
+        return {budgetBytes: this.denseUsed + this.expertUsed, densePlannedBytes: this.denseUsed,
+            denseResidentBytes: this.denseUsed, expertResidentBytes: this.expertUsed,
+            residentExperts: Array.from(this.tensors.keys()).filter(n => /\.expert\.\d+\.gate$/.test(n)).length,
+            hits: this.hits, misses: this.misses, evictions: this.evictions};
+    }
+    async dispose() {
+        for (const buffer of this.tensors.values()) this.b.free(buffer);
+        this.tensors.clear(); this.denseUsed = 0; this.expertUsed = 0;
+    }
+}

@@ -45,7 +45,12 @@ def test_kernel_table_lists_reference_kernels():
     for name in ["strata_project", "strata_router", "strata_router_batch", "strata_q2_gate_up", "strata_q2_down",
                  "strata_moe_combine", "strata_moe_combine_batch", "strata_gather_rows", "strata_scatter_rows",
                  "strata_unpack_half", "strata_expert_scales", "strata_q2_project", "strata_quant_project",
-                 "strata_norm", "strata_elementwise", "strata_gemv"]:
+                 "strata_norm", "strata_elementwise", "strata_gemv",
+                 # the fixture model's kernels outside the MoE path
+                 "strata_embedding", "strata_rope_frequencies", "strata_rope_table", "strata_rope_position",
+                 "strata_hc_mix", "strata_hc_write", "strata_conv", "strata_gdn_gates", "strata_gdn_step",
+                 "strata_slice", "strata_kv_append", "strata_attention", "strata_attention_gate", "strata_ple_gate",
+                 "strata_ple_broadcast", "strata_ple_add", "strata_argmax"]:
         assert name in sigs, name
 
 
