@@ -82,7 +82,15 @@ int sm_sync(sm_ctx *ctx);
  * args holds one 64-bit slot per parameter in the reference's parameter order:
  * a buffer handle for pointer parameters, the int32 or float32 bit pattern in
  * the low 32 bits for scalars. sm_kernel_signature gives the parameter list
- * as "Name:type,..." with types f32*, i32*, u32*, i32 and f32. */
+ * as "Name:type,..." with types f32*, i32*, u32*, i32 and f32.
+ * The kernels: the 16 on the MoE path (strata_project, strata_router, the Q2
+ * expert family, strata_norm, strata_elementwise, strata_moe_combine, ...)
+ * and the 17 that StrataEngine.step (src/engine.js:76-196) launches besides
+ * them for the untrained fixture model (strata_embedding, strata_rope_*,
+ * strata_hc_*, strata_conv, strata_gdn_*, strata_slice, strata_kv_append,
+ * strata_attention[_gate], strata_ple_gate/_broadcast/_add, strata_argmax);
+ * sm_kernel_name lists them. Cells / Mapping / Indices buffers are checked
+ * on the device before use (SM_E_BOUNDS), which synchronises the stream. */
 int sm_run(sm_ctx *ctx, const char *name, const uint32_t groups[3], const uint64_t *args, int nargs);
 int sm_kernel_count(void);
 const char *sm_kernel_name(int index);
