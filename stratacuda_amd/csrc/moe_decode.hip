@@ -206,7 +206,8 @@ constexpr int GU_WAVES = 4; // waves per block -> 16 hidden rows per block
 // Four hidden rows j0..j0+3 of one expert by one wave. Lane (half = lane/32,
 // gl = lane%32) covers group gl (then gl + 32, ...) of gate row j (half 0)
 // or up row j (half 1); `first` is the lane's first group, loaded early.
-__device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, const XQ &first, const uint8_t *blob,
+__device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, const XQ &first, const XQ &second,
+                                             const uint8_t *blob,
                                              uint64_t gu_scales, float *__restrict__ hidden_row, int j0, int width,
                                              int ff, const uint64_t *tab) {
     const int lane = threadIdx.x & 63, half = lane >> 5, gl = lane & 31;
@@ -229,10 +230,24 @@ __device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, co
     };
     if (blob) {
         if (gl < G) group(gl, first);
-        for (int g = gl + 32; g < G; g += 32) {
-            XQ q;
-            load_xq(xq, g, q);
-            group(g, q);
+        if (G > 32 && G <= 40) {
+            // 33-40 groups (the real model's 2560 = 40): the (row, group)
+            // pairs of groups 32.. are spread one per lane instead of a
+            // second pass over the first lanes, so every lane makes five code
+            // loads. `second` is the lane's record, loaded with `first`.
+            const int G2 = G - 32, item = gl < 4 * G2 ? gl : 0, r2 = item / G2, g2 = 32 + item % G2;
+            const int wrow = 2 * min(j0 + r2, ff - 1) + half;
+            const uint4 c = load_codes(blob + (uint64_t)wrow * row_bytes + (uint64_t)g2 * 16);
+            const uint32_t sb = *(const uint16_t *)(blob + gu_scales + ((uint64_t)wrow * G + g2) * 2);
+            const float v = gl < 4 * G2 ? sm::half_bits(sb) * dot64_q(c, second) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < GU_ROWS; r++) acc[r] += r == r2 ? v : 0.0f;
+        } else {
+            for (int g = gl + 32; g < G; g += 32) {
+                XQ q;
+                load_xq(xq, g, q);
+                group(g, q);
+            }
         }
     }
     // Row r's gate and up sums (lanes 31 and 63 after the half-wave sums)
@@ -352,8 +367,13 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
     // and the block reads its slot's ID instead of selecting it itself.
     float lg[8];
     if (k < topk && !routed) sm::router_load(logits, experts, lg);
-    XQ first;
+    XQ first, second;
     load_xq(xq, min(gl, width / 64 - 1), first);  // unconditional: the wait for the logits leaves these in flight
+    {
+        // Groups 32..39 of widths 2112..2560: the lane's item of the second set.
+        const int G2 = width / 64 - 32;
+        if (G2 > 0 && G2 <= 8) load_xq(xq, 32 + (gl < 4 * G2 ? gl : 0) % G2, second);
+    }
     sm::fill_exp_table(s_tab);
     if (k < topk && routed) {
         if (threadIdx.x == 0) s_ids[k] = ids[k];
@@ -364,7 +384,7 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
     const uint8_t *blob = slot_blob(arena, stride, shared_blob, k < topk ? s_ids[k] : 0, k, topk, experts);
     const int j0 = (blockIdx.x * GU_WAVES + wave) * GU_ROWS;
     if (j0 < ff)
-        gate_up_rows(xq, first, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
+        gate_up_rows(xq, first, second, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
     // Block (0, 0) publishes the token's IDs and routing weights, after its
     // own expert work so that no block's loads wait for the weights.
     if (k == 0 && !routed && blockIdx.x == 0 && wave == 0) {
@@ -384,10 +404,11 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
 struct CombineIn {
     float w, gate, res;
 };
+template <int ROWS = 8>
 __device__ __forceinline__ CombineIn combine_load(const float *__restrict__ weights, const float *__restrict__ gate,
                                                   const float *__restrict__ resid, int width, int topk) {
     const int tid = threadIdx.x;
-    const int row = min((int)blockIdx.x * 8 + (tid & 7), width - 1);
+    const int row = min((int)blockIdx.x * ROWS + (tid & 7) % ROWS, width - 1);
     CombineIn in;
     in.w = weights[min(tid, topk - 1)];
     in.gate = gate[0];
@@ -401,14 +422,16 @@ __device__ __forceinline__ float combine_stage(const CombineIn &in, float *s_w, 
     if (tid < topk) s_w[tid] = in.w;
     return tid < 8 ? sm::sigmoid(in.gate, s_tab) : 0.0f;
 }
+// parts[k * ROWS + r]: slot k's value of the block's row r.
+template <int ROWS = 8>
 __device__ __forceinline__ void down_combine(const float *parts, const float *s_w, float sig, const CombineIn &in,
                                              float *__restrict__ Y, int width, int topk, bool has_resid) {
     const int tid = threadIdx.x;
-    if (tid < 8) {
-        const int row = blockIdx.x * 8 + tid;
+    if (tid < ROWS) {
+        const int row = blockIdx.x * ROWS + tid;
         if (row < width) {
-            float value = parts[topk * 8 + tid] * sig;
-            for (int k = 0; k < topk; k++) value = value + parts[k * 8 + tid] * s_w[k];
+            float value = parts[topk * ROWS + tid] * sig;
+            for (int k = 0; k < topk; k++) value = value + parts[k * ROWS + tid] * s_w[k];
             Y[row] = has_resid ? in.res + value : value;
         }
     }
@@ -526,6 +549,108 @@ __global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down(const float *__re
     down_combine(parts, s_w, sig, cin, Y, width, topk, resid != nullptr);
 }
 
+// K3 for 9-10 groups per down row (the real model's ff 640). Grid
+// ceil(width / 6), 512 threads, 6 output rows per block; lane (rr = lane / 10,
+// gl = lane % 10) dots group gl of down row rr with group gl of the slot's
+// hidden vector (lanes 60-63 idle). Wave w handles slots w, w+8. A slot's
+// hidden vector comes into a wave-private LDS area by one cooperative load
+// (10 values per lane); the 10 partial sums of a row are added in order by
+// its first lane through a wave-private LDS line.
+constexpr int D10_ROWS = 6;
+template <int NQ>
+__global__ void __launch_bounds__(64 * DN_WAVES) k_decode_down10(const float *__restrict__ hidden,
+                                                                const uint8_t *__restrict__ arena, uint64_t stride,
+                                                                const uint8_t *__restrict__ shared_blob,
+                                                                const int *__restrict__ ids,
+                                                                const float *__restrict__ weights,
+                                                                const float *__restrict__ gate, float *__restrict__ Y,
+                                                                int width, int ff, int topk, int experts,
+                                                                uint64_t down_codes, uint64_t down_scales,
+                                                                const float *__restrict__ resid) {
+    static_assert(NQ >= 1 && NQ <= DN_MAX_SLOTS, "slots per wave");
+    {  // token blockIdx.y
+        const int t = blockIdx.y;
+        hidden += (uint64_t)t * (topk + 1) * ff;
+        ids += (int64_t)t * topk;
+        weights += (int64_t)t * topk;
+        gate += t;
+        Y += (int64_t)t * width;
+        if (resid) resid += (int64_t)t * width;
+    }
+    __shared__ float parts[33 * D10_ROWS];
+    __shared__ float s_w[32];
+    __shared__ uint64_t s_tab[32];
+    __shared__ __attribute__((aligned(16))) float s_h[DN_WAVES][10 * DN_PITCH];
+    __shared__ float s_red[DN_WAVES][64];
+    const int nexp = topk + 1, GF = ff / 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rr = lane / 10, gl = lane - 10 * rr;
+    const bool live = rr < D10_ROWS && gl < GF;
+    const int r = min((int)blockIdx.x * D10_ROWS + min(rr, D10_ROWS - 1), width - 1);
+    const int gc = min(gl, GF - 1);
+    const uint64_t row_bytes = (uint64_t)ff / 4;
+    const int my_id = ids[min(lane, topk - 1)];
+    const CombineIn cin = combine_load<D10_ROWS>(weights, gate, resid, width, topk);
+    // Values 10 lane .. 10 lane + 9 of every slot's hidden vector (clamped
+    // addresses past ff; those values are never stored).
+    float2 hq[NQ][5];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const float *src = hidden + (uint64_t)min(wave + DN_WAVES * q, nexp - 1) * ff;
+#pragma unroll
+        for (int i = 0; i < 5; i++) hq[q][i] = *(const float2 *)(src + min(10 * lane + 2 * i, ff - 2));
+    }
+    uint4 c[NQ];
+    uint32_t sb[NQ];
+    bool ok[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const int k = wave + DN_WAVES * q;
+        const int lid = __builtin_amdgcn_readlane(my_id, min(k, 63));
+        const int id = k < topk ? lid : 0;
+        const uint8_t *blob = k < nexp ? slot_blob(arena, stride, shared_blob, id, k, topk, experts) : shared_blob;
+        ok[q] = blob != nullptr;
+        blob = blob ? blob : shared_blob;  // an invalid ID reads the shared blob; the slot yields NaN
+        c[q] = load_codes(blob + down_codes + (uint64_t)r * row_bytes + (uint64_t)gc * 16);
+        sb[q] = *(const uint16_t *)(blob + down_scales + ((uint64_t)r * GF + gc) * 2);
+    }
+    sm::fill_exp_table(s_tab);
+    float *xh = s_h[wave], *red = s_red[wave];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const int k = wave + DN_WAVES * q;
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            const int idx = 10 * lane + 2 * i;  // even, so both values share a group
+            if (idx < ff) *(float2 *)&xh[(idx >> 6) * DN_PITCH + (idx & 63)] = hq[q][i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        float h[64];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = *(const float4 *)&xh[gc * DN_PITCH + 4 * i];
+            h[4 * i] = v.x;
+            h[4 * i + 1] = v.y;
+            h[4 * i + 2] = v.z;
+            h[4 * i + 3] = v.w;
+        }
+        float v = ok[q] ? 0.0f : __builtin_nanf("");
+        if (ok[q] && live) v = sm::half_bits(sb[q]) * (dot64_4(c[q], h) - sum64(h));
+        red[lane] = v;
+        __builtin_amdgcn_wave_barrier();
+        if (gl == 0 && rr < D10_ROWS && k < nexp) {
+            float t = red[lane];
+            for (int j = 1; j < GF; j++) t = t + red[lane + j];
+            parts[k * D10_ROWS + rr] = t;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    const float sig = combine_stage(cin, s_w, topk, s_tab);
+    __syncthreads();
+    down_combine<D10_ROWS>(parts, s_w, sig, cin, Y, width, topk, resid != nullptr);
+}
+
 // K3 for any other shape: hidden groups read from memory, lanes loop over
 // groups gl, gl+8, ... of row r.
 __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restrict__ hidden,
@@ -620,8 +745,11 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
         const dim3 grid((unsigned)((route_blocks + ceil_div(width / 64, 4) + 7) / 8 * 8), (unsigned)tokens);
         using K1 = void (*)(const float *, const float *, const float *, const float *, float *, float *, uint32_t *,
                             int, int, int, const float *, float);
-        const K1 k1 = width == 2048 ? (gamma ? k_decode_route<32, true> : k_decode_route<32, false>)
-                                    : (gamma ? k_decode_route<0, true> : k_decode_route<0, false>);
+        // Register-resident rows for the benchmark width (32 groups) and the
+        // real model's (2560: 40 groups); a strided loop otherwise.
+        const K1 k1 = width == 2048   ? (gamma ? k_decode_route<32, true> : k_decode_route<32, false>)
+                      : width == 2560 ? (gamma ? k_decode_route<40, true> : k_decode_route<40, false>)
+                                      : (gamma ? k_decode_route<0, true> : k_decode_route<0, false>);
         k1<<<grid, 256, 0, ctx->stream>>>((const float *)X, (const float *)Wr, (const float *)bias, (const float *)Wsg,
                                           (float *)(ws + w.logits), (float *)(ws + w.gate), xq, width, experts,
                                           route_blocks, gamma, eps);
@@ -651,9 +779,13 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
                             const float *, float *, int, int, int, int, uint64_t, uint64_t, const float *);
         static const K3 by_slots[DN_MAX_SLOTS] = {k_decode_down<1>, k_decode_down<2>, k_decode_down<3>,
                                                   k_decode_down<4>, k_decode_down<5>};
-        const bool narrow = ff <= 512;
-        const K3 kernel = narrow ? by_slots[ceil_div(topk + 1, DN_WAVES) - 1] : k_decode_down_wide;
-        kernel<<<dim3((unsigned)ceil_div(width, 8), (unsigned)tokens), narrow ? 64 * DN_WAVES : 256, 0, ctx->stream>>>(
+        static const K3 by_slots10[DN_MAX_SLOTS] = {k_decode_down10<1>, k_decode_down10<2>, k_decode_down10<3>,
+                                                    k_decode_down10<4>, k_decode_down10<5>};
+        const bool narrow = ff <= 512, ten = ff > 512 && ff <= 640;
+        const int nq = ceil_div(topk + 1, DN_WAVES) - 1, rows = ten ? D10_ROWS : 8;
+        const K3 kernel = narrow ? by_slots[nq] : ten ? by_slots10[nq] : k_decode_down_wide;
+        kernel<<<dim3((unsigned)ceil_div(width, rows), (unsigned)tokens), narrow || ten ? 64 * DN_WAVES : 256, 0,
+                 ctx->stream>>>(
             hidden, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const int *)ids,
             (const float *)weights, (const float *)(ws + w.gate), (float *)Y, width, ff, topk, experts, L.down_codes,
             L.down_scales, resid);
