@@ -343,7 +343,30 @@ __device__ __forceinline__ void ring_sync() {
     asm volatile("" ::: "memory");
 }
 
-constexpr int STREAM_MAX_G = 32;  // K <= 2048 for the streaming kernel
+constexpr int STREAM_MAX_G = 40;  // K <= 2560 for the streaming kernels (the real model's width)
+
+// The G fp16 scales of one weight row (2G contiguous bytes) into G/2 words:
+// 16-byte loads when a row is a whole number of them (G % 8 == 0), else
+// 4-byte loads (G even: rows start 4-byte aligned).
+template <int G>
+__device__ __forceinline__ void load_row_scales(const uint8_t *p, uint32_t (&s)[G / 2]) {
+    static_assert(G % 2 == 0, "an even number of groups");
+    if constexpr (G % 8 == 0) {
+        const uint4 *sp = (const uint4 *)p;
+#pragma unroll
+        for (int c = 0; c < G / 8; c++) {
+            const uint4 v = sp[c];
+            s[4 * c + 0] = v.x;
+            s[4 * c + 1] = v.y;
+            s[4 * c + 2] = v.z;
+            s[4 * c + 3] = v.w;
+        }
+    } else {
+        const uint32_t *sp = (const uint32_t *)p;
+#pragma unroll
+        for (int c = 0; c < G / 2; c++) s[c] = sp[c];
+    }
+}
 
 // Ring stages. Each stage is a separate object at namespace scope: the
 // compiler's wait insertion then tells loads into one stage from reads of
@@ -412,7 +435,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     constexpr int BM = P::BM, BN = P::BN, ACH = P::ACH, BCH = P::BCH;
     using Stage = RingStage<BM>;
     constexpr int NS = Ring<BM>::NS;
-    static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 8 == 0, "K / 64 groups");
+    static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 2 == 0, "K / 64 groups");
     static_assert(BM <= 64 && BN <= 256, "stage size");
     // Tile record (segment, first row, end of the segment) from the dispatch.
     const int tau = blockIdx.y;
@@ -457,17 +480,8 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     // ring's first wait also covers them.
     uint32_t sreg[NI][G / 2];
 #pragma unroll
-    for (int ni = 0; ni < NI; ni++) {
-        const uint4 *sp = (const uint4 *)(blob + scales_off + (uint64_t)(n0 + wave * 32 * NI + ni * 32 + j) * G * 2);
-#pragma unroll
-        for (int c = 0; c < G / 8; c++) {
-            const uint4 v = sp[c];
-            sreg[ni][4 * c + 0] = v.x;
-            sreg[ni][4 * c + 1] = v.y;
-            sreg[ni][4 * c + 2] = v.z;
-            sreg[ni][4 * c + 3] = v.w;
-        }
-    }
+    for (int ni = 0; ni < NI; ni++)
+        load_row_scales<G>(blob + scales_off + (uint64_t)(n0 + wave * 32 * NI + ni * 32 + j) * G * 2, sreg[ni]);
 #pragma clang loop unroll(full)
     for (int q = 0; q < NS - 1; q++) with_stage<BM>(q, [&](Stage &sg) { issue(sg, min(q, G - 1)); });
 
@@ -576,7 +590,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
     using Stage = RingStage<BM>;
     constexpr int NS = Ring<BM>::NS;
     constexpr int G = KG;  // K / 64
-    static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 8 == 0, "K / 64 groups");
+    static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 2 == 0, "K / 64 groups");
     (void)K;
     (void)N;
     // Tile record (segment, first row, end of the segment) from the dispatch.
@@ -607,17 +621,8 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
     // Scales of the lane's four weight rows, every group, in registers.
     uint32_t sreg[NT][G / 2];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const uint4 *sp = (const uint4 *)(blob + scales_off + (uint64_t)(n0 + wave * 64 + nt * 16 + col) * G * 2);
-#pragma unroll
-        for (int c = 0; c < G / 8; c++) {
-            const uint4 v = sp[c];
-            sreg[nt][4 * c + 0] = v.x;
-            sreg[nt][4 * c + 1] = v.y;
-            sreg[nt][4 * c + 2] = v.z;
-            sreg[nt][4 * c + 3] = v.w;
-        }
-    }
+    for (int nt = 0; nt < NT; nt++)
+        load_row_scales<G>(blob + scales_off + (uint64_t)(n0 + wave * 64 + nt * 16 + col) * G * 2, sreg[nt]);
 #pragma clang loop unroll(full)
     for (int q = 0; q < NS - 1; q++) with_stage<BM>(q, [&](Stage &sg) { issue(sg, min(q, G - 1)); });
 
@@ -822,11 +827,12 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                                                                             (_Float16 *)(ws + w.Xhl), groups);
     int *offsets = (int *)(ws + w.offsets);
     int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);
-    // Streaming kernels: N a multiple of 256 and K of 2048 or 512 in both
-    // products. Segments of up to 32 rows then run in 16-row tiles, else in
-    // one 32-row tile; longer ones in 64-row tiles.
-    const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && (width == 2048 || width == 512) &&
-                        (ff == 2048 || ff == 512);
+    // Streaming kernels: N a multiple of 256 and K one of the compiled group
+    // counts in both products (512, 640, 2048, 2560: the benchmark's and the
+    // real model's shapes). Segments of up to 32 rows then run in 16-row
+    // tiles, else in one 32-row tile; longer ones in 64-row tiles.
+    auto streamable = [](int k) { return k == 512 || k == 640 || k == 2048 || k == 2560; };
+    const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && streamable(width) && streamable(ff);
     const int4 *info_small = (const int4 *)(ws + w.info_small), *info_big = (const int4 *)(ws + w.info_big);
     const int split = stream ? tiling_split(tokens) : 33;
     GemmTiling tiling = {tiles_small, tiles_big, split, stream ? 16 : 32, 64};
@@ -852,8 +858,18 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
                      void *out, int ld) -> int {
         if (stream) {
-            auto kb = gate_up ? (K == 2048 ? k_moe_gemm_stream<true, 2, 2, 32> : k_moe_gemm_stream<true, 2, 2, 8>)
-                              : (K == 2048 ? k_moe_gemm_stream<false, 2, 2, 32> : k_moe_gemm_stream<false, 2, 2, 8>);
+            using KT = decltype(&k_moe_gemm_stream<true, 2, 2, 8>);
+            const KT big_gu[4] = {k_moe_gemm_stream<true, 2, 2, 8>, k_moe_gemm_stream<true, 2, 2, 10>,
+                                  k_moe_gemm_stream<true, 2, 2, 32>, k_moe_gemm_stream<true, 2, 2, 40>};
+            const KT big_dn[4] = {k_moe_gemm_stream<false, 2, 2, 8>, k_moe_gemm_stream<false, 2, 2, 10>,
+                                  k_moe_gemm_stream<false, 2, 2, 32>, k_moe_gemm_stream<false, 2, 2, 40>};
+            using KS = decltype(&k_moe_gemm_stream16<true, 8>);
+            const KS small_gu[4] = {k_moe_gemm_stream16<true, 8>, k_moe_gemm_stream16<true, 10>,
+                                    k_moe_gemm_stream16<true, 32>, k_moe_gemm_stream16<true, 40>};
+            const KS small_dn[4] = {k_moe_gemm_stream16<false, 8>, k_moe_gemm_stream16<false, 10>,
+                                    k_moe_gemm_stream16<false, 32>, k_moe_gemm_stream16<false, 40>};
+            const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
+            const KT kb = gate_up ? big_gu[kv] : big_dn[kv];
             // The two tilings cover disjoint rows: the big-tile grid (few,
             // long blocks at small T) runs on the second stream beside the
             // small-tile grid.
@@ -864,8 +880,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                     a, r, info_big, tiles_big, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
                 rc_big = launched(ctx);
             }
-            auto ks = gate_up ? (K == 2048 ? k_moe_gemm_stream16<true, 32> : k_moe_gemm_stream16<true, 8>)
-                              : (K == 2048 ? k_moe_gemm_stream16<false, 32> : k_moe_gemm_stream16<false, 8>);
+            const KS ks = gate_up ? small_gu[kv] : small_dn[kv];
             int rc_small = SM_OK;
             if (rc_big == SM_OK) {
                 ks<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(

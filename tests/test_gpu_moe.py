@@ -223,7 +223,10 @@ def test_layer_small_batch_full(backend, oracle, full_layer, tokens):
 
 
 @pytest.mark.parametrize("W,F,E,topk,tokens", [(512, 512, 24, 4, 40), (2048, 2048, 8, 2, 33),
-                                               (512, 2048, 12, 3, 100), (2048, 512, 20, 4, 48)])
+                                               (512, 2048, 12, 3, 100), (2048, 512, 20, 4, 48),
+                                               # the real model's widths: 40 and 10 groups
+                                               (2560, 640, 20, 4, 70), (2048, 640, 16, 3, 48),
+                                               (2560, 512, 16, 3, 40)])
 def test_layer_stream_geometries(backend, oracle, W, F, E, topk, tokens):
     # Every (width, ff) pair of the streaming kernels, with and without the
     # K split, against the oracle on all tokens.
