@@ -22,7 +22,10 @@ read from profiles/traffic.json when present.
 prefill: T=512 (uniform routing) and T=2048 (Zipf(1.1) router prior) through
 the grouped-MFMA path, per-stage times from events, reported beside the main
 line. stack: the 48 resident layers chained (RMSNorm, MoE layer, residual) for
-128 steps at batch 1 and batch 32, one HIP graph per step. cpu_baseline: the CPU oracle (a restatement of the reference kernels in
+128 steps at batch 1 and batch 32, one HIP graph per step. real_model: the
+real model's geometry (hidden 2560, ff 640) through the same kernels, decode
+T=1 over 16 rotated resident layers and prefill T=512 / T=2048 (Zipf).
+cpu_baseline: the CPU oracle (a restatement of the reference kernels in
 their operation order, OpenMP over workgroups) on the host cores, T=1 decode
 of a bounded token sample of the same layer.
 """
@@ -62,6 +65,104 @@ def layer_bytes(W, F, E, K, T, distinct):
 
 def layer_flops(W, F, E, K, T):
     return T * ((K + 1) * 3 * 2 * W * F + 2 * E * W)
+
+
+def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefill_reps=4):
+    """The real model's geometry (hidden 2560, expert ff 640, 512 experts,
+    top-10 + shared, 1,382,400-byte Q2 blobs) through the same kernels:
+    decode T=1 rotating through `layers` resident layers (HIP graphs), the
+    decode kernels one stage at a time, and prefill T=512 / T=2048 (Zipf)."""
+    W, F, E, K = 2560, 640, 512, 10
+    lays = [wl.DeviceLayer(be, l, width=W, ff=F, experts=E, base_seed=wl.BASE_SEED + 1) for l in range(layers)]
+    slots = []
+    for i in range(layers):
+        x = be.alloc(W, zero=False)
+        be.synth_normal(x, W, lays[i].seed + 99, wl.STREAM_INPUT, 1.0)
+        slots.append({"x": x, "y": be.alloc(W), "ids": be.alloc(K, "i32"), "w": be.alloc(K),
+                      "ws": be.alloc_bytes(be.moe_workspace_bytes(1, W, F, E, K))})
+
+    def step(i):
+        s, lay = slots[i], lays[i]
+        be.moe_layer(s["x"], 1, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, s["y"], s["ids"],
+                     s["w"], s["ws"])
+
+    def all_layers():
+        for i in range(layers):
+            step(i)
+
+    all_layers()
+    be.sync()
+    g = capture(all_layers)
+    replay(g)
+    be.sync()
+    be.event_record(8)
+    for _ in range(steps // layers):
+        replay(g)
+    be.event_record(9)
+    be.sync()
+    release(g)
+    us = be.event_elapsed_ms(8, 9) * 1e3 / (steps // layers * layers)
+    step_bytes = layer_bytes(W, F, E, K, 1, K)
+    out = {"workload": "single MoE layer, hidden 2560, ff 640, 512 experts, top-10 + shared, Q2 (1,382,400-byte "
+                       "blobs), %d resident layers rotated" % layers,
+           "decode_T1": {"tokens_per_s": round(1e6 / us, 1), "us_per_step": round(us, 3),
+                         "hbm": {"bytes_per_step": step_bytes, "frac": round(step_bytes / (us * 1e-6) / PEAK_HBM, 4)}}}
+    kb = decode_kernel_bytes(W, F, E, K)
+    kern = {}
+    for stage, name in enumerate(["decode_route", "decode_gate_up", "decode_down_combine"]):
+        be.stage_select(1 << stage)
+        gid = capture(all_layers)
+        be.stage_select()
+        be.stage_select(1 << stage)
+        replay(gid)
+        be.sync()
+        be.event_record(8)
+        for _ in range(20):
+            replay(gid)
+        be.event_record(9)
+        be.sync()
+        be.stage_select()
+        kus = be.event_elapsed_ms(8, 9) * 1e3 / (20 * layers)
+        kern[name] = {"avg_us": round(kus, 3), "frac_hbm": round(kb[name] / (kus * 1e-6) / PEAK_HBM, 4)}
+        release(gid)
+    out["decode_T1"]["kernels"] = kern
+    for T, zipf in [(512, False), (2048, True)]:
+        X = be.alloc(T * W, zero=False)
+        be.synth_normal(X, T * W, wl.BASE_SEED + 5 + T, wl.STREAM_INPUT, 1.0)
+        bias = be.alloc(wl.zipf_bias(E, lays[0].seed)) if zipf else None
+        Y, ids, w = be.alloc(T * W), be.alloc(T * K, "i32"), be.alloc(T * K)
+        ws = be.alloc_bytes(be.moe_workspace_bytes(T, W, F, E, K))
+
+        def run(j):
+            lay = lays[j % layers]
+            be.moe_layer(X, T, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, Y, ids, w, ws,
+                         bias=bias)
+
+        for j in range(2):
+            run(j)
+        be.sync()
+        gp = capture(lambda: [run(j) for j in range(prefill_reps)])
+        replay(gp)
+        be.sync()
+        be.event_record(8)
+        replay(gp)
+        be.event_record(9)
+        be.sync()
+        release(gp)
+        ms = be.event_elapsed_ms(8, 9) / prefill_reps
+        distinct = len(np.unique(be.read(ids)))
+        lb, lf = layer_bytes(W, F, E, K, T, distinct), layer_flops(W, F, E, K, T)
+        out["prefill T=%d%s" % (T, " zipf" if zipf else "")] = {
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_layer": round(ms, 4), "distinct_experts": int(distinct),
+            "hbm_frac": round(lb / (ms * 1e-3) / PEAK_HBM, 4), "mfma_layer_frac": round(lf / (ms * 1e-3) / PEAK_MFMA_F16, 4)}
+        for b in (X, Y, ids, w, ws) + ((bias,) if bias is not None else ()):
+            be.free(b)
+    for s_ in slots:
+        for b in s_.values():
+            be.free(b)
+    for lay in lays:
+        lay.free()
+    return out
 
 
 def read_traffic(kernel):
@@ -258,6 +359,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack runs")
     ap.add_argument("--stack-steps", type=int, default=128)
+    ap.add_argument("--no-real", action="store_true",
+                    help="skip the real model's geometry (hidden 2560, ff 640) runs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="issue every step directly instead of replaying HIP graphs (for profilers)")
@@ -502,6 +605,10 @@ def main():
             be.free(inputs)
             st.free()
 
+    real = None
+    if not args.no_real:
+        real = real_model(be, wl, np, capture, replay, release)
+
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -530,6 +637,7 @@ def main():
         "kernels": kernels,
         "prefill": prefill,
         "stack": stack,
+        "real_model": real,
     }
     print(json.dumps(out))
     be.dispose()

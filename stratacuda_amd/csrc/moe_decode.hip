@@ -206,6 +206,7 @@ constexpr int GU_WAVES = 4; // waves per block -> 16 hidden rows per block
 // Four hidden rows j0..j0+3 of one expert by one wave. Lane (half = lane/32,
 // gl = lane%32) covers group gl (then gl + 32, ...) of gate row j (half 0)
 // or up row j (half 1); `first` is the lane's first group, loaded early.
+template <bool EXTRA>
 __device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, const XQ &first, const XQ &second,
                                              const uint8_t *blob,
                                              uint64_t gu_scales, float *__restrict__ hidden_row, int j0, int width,
@@ -230,7 +231,7 @@ __device__ __forceinline__ void gate_up_rows(const uint32_t *__restrict__ xq, co
     };
     if (blob) {
         if (gl < G) group(gl, first);
-        if (G > 32 && G <= 40) {
+        if (EXTRA) {
             // 33-40 groups (the real model's 2560 = 40): the (row, group)
             // pairs of groups 32.. are spread one per lane instead of a
             // second pass over the first lanes, so every lane makes five code
@@ -343,6 +344,9 @@ __global__ void __launch_bounds__(256) k_decode_route(const float *__restrict__ 
 // top-k into LDS (block (0,0) also writes ids / weights to memory), then every
 // wave computes 4 hidden rows of that routed expert. Slot topk is the shared
 // expert and needs no routing.
+// EXTRA: 33-40 groups per row (the real model's 2560), whose groups 32..
+// are spread one (row, group) pair per lane.
+template <bool EXTRA>
 __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restrict__ xq,
                                                         const uint8_t *__restrict__ arena, uint64_t stride,
                                                         const uint8_t *__restrict__ shared_blob,
@@ -369,10 +373,10 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
     if (k < topk && !routed) sm::router_load(logits, experts, lg);
     XQ first, second;
     load_xq(xq, min(gl, width / 64 - 1), first);  // unconditional: the wait for the logits leaves these in flight
-    {
+    if (EXTRA) {
         // Groups 32..39 of widths 2112..2560: the lane's item of the second set.
         const int G2 = width / 64 - 32;
-        if (G2 > 0 && G2 <= 8) load_xq(xq, 32 + (gl < 4 * G2 ? gl : 0) % G2, second);
+        load_xq(xq, 32 + (gl < 4 * G2 ? gl : 0) % G2, second);
     }
     sm::fill_exp_table(s_tab);
     if (k < topk && routed) {
@@ -384,7 +388,7 @@ __global__ void __launch_bounds__(256) k_decode_gate_up(const uint32_t *__restri
     const uint8_t *blob = slot_blob(arena, stride, shared_blob, k < topk ? s_ids[k] : 0, k, topk, experts);
     const int j0 = (blockIdx.x * GU_WAVES + wave) * GU_ROWS;
     if (j0 < ff)
-        gate_up_rows(xq, first, second, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
+        gate_up_rows<EXTRA>(xq, first, second, blob, gu_scales, hidden + (uint64_t)k * ff, j0, width, ff, s_tab);
     // Block (0, 0) publishes the token's IDs and routing weights, after its
     // own expert work so that no block's loads wait for the weights.
     if (k == 0 && !routed && blockIdx.x == 0 && wave == 0) {
@@ -767,7 +771,9 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
     if (stage_on(ctx, kStageDecodeGateUp)) {
         if (int rc = stage_mark(ctx, kStageDecodeGateUp)) return rc;
         dim3 g1((unsigned)blocks_per_expert, (unsigned)(topk + 1), (unsigned)tokens);
-        k_decode_gate_up<<<g1, 64 * GU_WAVES, 0, ctx->stream>>>(
+        const int G = width / 64;
+        const auto k2 = G > 32 && G <= 40 ? k_decode_gate_up<true> : k_decode_gate_up<false>;
+        k2<<<g1, 64 * GU_WAVES, 0, ctx->stream>>>(
             xq, (const uint8_t *)arena, blob_stride, (const uint8_t *)shared_blob, (const float *)(ws + w.logits),
             (int *)ids, (float *)weights, hidden, width, ff, topk, experts, L.gate_up_scales, routed);
         if (int rc = launched(ctx)) return rc;
