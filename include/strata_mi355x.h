@@ -96,6 +96,20 @@ int sm_kernel_count(void);
 const char *sm_kernel_name(int index);
 const char *sm_kernel_signature(const char *name);
 
+/* ------------------------------------------------------- pack loading */
+/* Streams `count` expert blobs of blob_bytes each, stored back to back at
+ * file_offset of the pack file `path` (experts.bin: a layer's 512 blobs from
+ * its manifest offset, vendor/strata/tools/pack_layer.py:68-115), into the
+ * arena: blob i at arena + dst_offset + i * stride. Then checks on the device
+ * that every fp16 scale of every blob (bytes [scales_offset, blob_bytes)) is
+ * finite; a non-finite scale fails with SM_E_ARG naming the first such blob.
+ * Replaces PackStore.readExpertBlob / prefetchExpert (src/model.js:120-167)
+ * and the per-expert upload of WeightResidency.loadExpert
+ * (src/residency.js:52-77): the whole layer becomes resident in one call.
+ * Synchronous (returns when the copies and the check are done). */
+int sm_load_experts(sm_ctx *ctx, const char *path, uint64_t file_offset, uint64_t blob_bytes, int count,
+                    uint64_t arena, uint64_t dst_offset, uint64_t stride, uint64_t scales_offset);
+
 /* ----------------------------------------------------------- MoE layer */
 /* Router: logits[t, e] = X[t,:] . Wr[e,:] (+ bias[e] when bias != 0) in the
  * reference's f32 operation order, then softmax, top-k by repeated argmax

@@ -81,6 +81,7 @@ def lib():
             "sm_synth_normal": (i, [vp, u64, u64, u64, u64, u64, ctypes.c_double]),
             "sm_synth_uniform_pm": (i, [vp, u64, u64, u64, u64, u64, ctypes.c_double]),
             "sm_synth_blobs": (i, [vp, u64, u64, u64, i, i, i, u64, u64, ctypes.c_double]),
+            "sm_load_experts": (i, [vp, ctypes.c_char_p, u64, u64, i, u64, u64, u64, u64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -347,6 +348,13 @@ class Backend:
 
     def synth_uniform_pm(self, buf, n, seed, stream, amp, offset_bytes=0):
         self._check(lib().sm_synth_uniform_pm(self._ctx, buf.handle, offset_bytes, n, seed, stream, amp))
+
+    def load_experts(self, path, file_offset, blob_bytes, count, arena, stride, scales_offset, dst_offset=0):
+        """Stream `count` blobs (back to back at file_offset of a pack's
+        experts.bin) into `arena` at `stride`, then check their fp16 scales
+        (PackStore.readExpertBlob, src/model.js:160-167)."""
+        self._check(lib().sm_load_experts(self._ctx, os.fsencode(path), file_offset, blob_bytes, count,
+                                          arena.handle, dst_offset, stride, scales_offset))
 
     def synth_blobs(self, buf, count, width, ff, seed, first_stream, sigma=0.05, stride=None, offset_bytes=0):
         stride = blob_layout(width, ff)["blob_bytes"] if stride is None else stride

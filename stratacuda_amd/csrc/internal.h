@@ -41,11 +41,17 @@ struct sm_ctx {
     // Instantiated HIP graphs (sm_graph_*); nullptr marks a freed slot.
     std::vector<hipGraphExec_t> graphs;
     bool capturing = false;
+    // Pinned staging buffers of sm_load_experts (allocated at first use) and
+    // the events that mark their copies done.
+    void *staging[2] = {nullptr, nullptr};
+    hipEvent_t staged[2] = {nullptr, nullptr};
 };
 
 namespace smi {
 
 int fail(sm_ctx *ctx, int code, const std::string &msg);
+// Frees the pack loader's staging buffers (sm_shutdown).
+void pack_release(sm_ctx *ctx);
 int hip_fail(sm_ctx *ctx, hipError_t err, const char *what);
 // Checks that `handle` is a live allocation holding at least `bytes` bytes.
 int need(sm_ctx *ctx, uint64_t handle, uint64_t bytes, const char *what);

@@ -135,6 +135,7 @@ void sm_shutdown(sm_ctx *ctx) {
     for (auto &kv : ctx->buffers) (void)hipFree((void *)kv.first);
     ctx->buffers.clear();
     if (ctx->counters) (void)hipFree(ctx->counters);
+    pack_release(ctx);
     for (auto &e : ctx->stage_pool) (void)hipEventDestroy(e);
     for (auto &g : ctx->graphs)
         if (g) (void)hipGraphExecDestroy(g);

@@ -177,3 +177,132 @@ class DeviceStack:
                 lay.free()
         for buf in self.H + self.ids + self.w + [self.Xn, self.Y, self.ws]:
             self.b.free(buf)
+
+
+# ---------------------------------------------------------------- packs
+# A pack on disk in the reference's strata-pack layout (vendor/strata/tools/
+# strata_pack.py:219-263, pack_layer.py:54-115): manifest.json, experts.bin
+# holding each layer's blobs back to back (layer l's blob e at the layer's
+# offset + e * blob_bytes), and dense.bin holding f32 ("P32") value planes of
+# the dense tensors. One extension for this workload, whose shared expert is a
+# Q2 blob like the routed ones: manifest.experts.shared lists each layer's
+# shared blob in experts.bin (after the routed blobs of every layer).
+PACK_FORMAT = "strata-pack"
+
+
+def blob_offsets(width, ff):
+    """Byte offsets of the four planes of a blob (pack_layer.py:54-65)."""
+    gu_codes = 0
+    d_codes = gu_codes + 2 * ff * width // 4
+    gu_scales = d_codes + width * ff // 4
+    d_scales = gu_scales + 2 * ff * (width // 64) * 2
+    return {"gate_up_codes": gu_codes, "down_codes": d_codes, "gate_up_scales": gu_scales, "down_scales": d_scales}
+
+
+def write_pack(path, width, ff, experts, topk, layers, name="synthetic MoE pack"):
+    """Writes a pack directory. ``layers``: one dict per layer with
+    ``arena`` (uint8, experts blobs at `stride`), ``stride``, ``shared``
+    (uint8 blob), ``Wr`` (f32 [experts x width]), ``Wsg`` and ``gamma``
+    (f32 [width])."""
+    import json
+    import os
+    os.makedirs(path, exist_ok=True)
+    bb = blob_bytes(width, ff)
+    man = {"format": PACK_FORMAT, "name": name,
+           "config": {"width": width, "ff": ff, "experts": experts, "topK": topk, "layers": len(layers)},
+           "tensors": {}, "n_experts_per_layer": experts}
+    exp_layers, shared, dense_at = [], [], 0
+    with open(os.path.join(path, "experts.bin"), "wb") as ef:
+        for l, lay in enumerate(layers):
+            arena = np.asarray(lay["arena"], np.uint8).reshape(experts, lay["stride"])[:, :bb]
+            exp_layers.append({"layer": l, "offset": ef.tell()})
+            ef.write(np.ascontiguousarray(arena).tobytes())
+        for l, lay in enumerate(layers):
+            shared.append({"layer": l, "offset": ef.tell()})
+            ef.write(np.asarray(lay["shared"], np.uint8)[:bb].tobytes())
+        experts_size = ef.tell()
+    with open(os.path.join(path, "dense.bin"), "wb") as df:
+        for l, lay in enumerate(layers):
+            for tname, key, shape in (("ffn_gate_inp.weight", "Wr", [width, experts]),
+                                      ("ffn_gate_inp_shexp.weight", "Wsg", [width]),
+                                      ("ffn_norm.weight", "gamma", [width])):
+                data = np.asarray(lay[key], np.float32).tobytes()
+                man["tensors"]["blk.%d.%s" % (l, tname)] = {
+                    "file": "dense.bin", "shape": shape, "form": "P32", "source_type": "F32",
+                    "values": {"offset": df.tell(), "bytes": len(data)}}
+                df.write(data)
+        dense_size = df.tell()
+    man["experts"] = {"blob_bytes": bb, "offsets": blob_offsets(width, ff), "layers": exp_layers,
+                      "total_bytes": len(layers) * experts * bb, "scales_fp16": True, "source_type": "Q2_0",
+                      "form": "S2", "shared": shared}
+    man["files"] = {"experts.bin": experts_size, "dense.bin": dense_size}
+    with open(os.path.join(path, "manifest.json"), "w") as f:
+        json.dump(man, f, indent=1)
+    return man
+
+
+class PackReader:
+    """Reads a pack directory with the checks of PackStore (src/model.js:82-103):
+    format and expert source type, file sizes against the manifest, plane
+    bounds, the blob layout against the geometry."""
+
+    def __init__(self, path):
+        import json
+        import os
+        self.path = path
+        self.manifest = man = json.load(open(os.path.join(path, "manifest.json")))
+        if man.get("format") != PACK_FORMAT:
+            raise ValueError("Expected a Strata canonical pack manifest")
+        ex = man.get("experts") or {}
+        if ex.get("source_type") != "Q2_0":
+            raise ValueError("Canonical expert import currently requires Q2_0; IQ expert packs are not supported")
+        c = man["config"]
+        self.width, self.ff, self.experts, self.topk, self.layers = (c["width"], c["ff"], c["experts"], c["topK"],
+                                                                    c["layers"])
+        if self.width % 64 or self.ff % 64:
+            raise ValueError("Packed expert dimensions must contain complete groups")
+        if ex["blob_bytes"] != blob_bytes(self.width, self.ff) or ex["offsets"] != blob_offsets(self.width, self.ff):
+            raise ValueError("expert blob layout does not match the geometry")
+        for name, size in man.get("files", {}).items():
+            if os.path.getsize(os.path.join(path, name)) != size:
+                raise ValueError(name + " size differs from manifest")
+        for name, t in man["tensors"].items():
+            p = t["values"]
+            if p["offset"] < 0 or p["offset"] + p["bytes"] > os.path.getsize(os.path.join(path, t["file"])):
+                raise ValueError("Invalid plane " + name + ".values")
+            if p["bytes"] != int(np.prod(t["shape"])) * 4:
+                raise ValueError("Invalid value plane size: " + name)
+        self.blob_bytes = ex["blob_bytes"]
+
+    def dense(self, layer, tname):
+        import os
+        t = self.manifest["tensors"]["blk.%d.%s" % (layer, tname)]
+        with open(os.path.join(self.path, t["file"]), "rb") as f:
+            f.seek(t["values"]["offset"])
+            data = np.frombuffer(f.read(t["values"]["bytes"]), np.float32).copy()
+        if not np.all(np.isfinite(data)):
+            raise ValueError("Non-finite model weights")
+        return data
+
+    def load_layer(self, backend, layer):
+        """The layer resident on the device (a DeviceLayer-shaped object):
+        its routed blobs streamed from experts.bin by sm_load_experts."""
+        import os
+        ex = self.manifest["experts"]
+        info = [e for e in ex["layers"] if e["layer"] == layer]
+        sh = [e for e in ex.get("shared", []) if e["layer"] == layer]
+        if not info or not sh:
+            raise ValueError("Layer %d is not in the pack" % layer)
+        lay = DeviceLayer.__new__(DeviceLayer)
+        lay.b, lay.width, lay.ff, lay.experts = backend, self.width, self.ff, self.experts
+        lay.seed, lay.stride = None, blob_stride(self.width, self.ff)
+        lay.arena = backend.alloc_bytes(lay.stride * self.experts)
+        lay.shared = backend.alloc_bytes(lay.stride)
+        f = os.path.join(self.path, "experts.bin")
+        scales = ex["offsets"]["gate_up_scales"]
+        backend.load_experts(f, info[0]["offset"], self.blob_bytes, self.experts, lay.arena, lay.stride, scales)
+        backend.load_experts(f, sh[0]["offset"], self.blob_bytes, 1, lay.shared, lay.stride, scales)
+        lay.Wr = backend.alloc(self.dense(layer, "ffn_gate_inp.weight"))
+        lay.Wsg = backend.alloc(self.dense(layer, "ffn_gate_inp_shexp.weight"))
+        lay.gamma = backend.alloc(self.dense(layer, "ffn_norm.weight"))
+        return lay
