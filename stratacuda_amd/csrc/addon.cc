@@ -452,6 +452,19 @@ napi_value SynthBlobs(napi_env env, napi_callback_info info) {
     if (!a.ok || fail(env, ctx, sm_synth_blobs(ctx, d, off, stride, count, width, ff, seed, first, s))) return nullptr;
     return undefined(env);
 }
+// loadExperts(ctx, path, fileOffset, blobBytes, count, arena, dstOffset, stride, scalesOffset)
+napi_value LoadExperts(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!a.need(9)) return nullptr;
+    sm_ctx *ctx = a.ctx(0);
+    const std::string path = a.str(1);
+    uint64_t foff = a.u64(2), bb = a.u64(3);
+    int count = a.i32(4);
+    uint64_t arena = a.u64(5), doff = a.u64(6), stride = a.u64(7), soff = a.u64(8);
+    if (!a.ok || fail(env, ctx, sm_load_experts(ctx, path.c_str(), foff, bb, count, arena, doff, stride, soff)))
+        return nullptr;
+    return undefined(env);
+}
 napi_value EventRecord(napi_env env, napi_callback_info info) {
     Args a(env, info);
     if (!a.need(2)) return nullptr;
@@ -529,6 +542,7 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
                {"synthNormal", SynthNormal},
                {"synthUniformPm", SynthUniformPm},
                {"synthBlobs", SynthBlobs},
+               {"loadExperts", LoadExperts},
                {"eventRecord", EventRecord},
                {"eventElapsed", EventElapsed},
                {"graphBegin", GraphBegin},

@@ -241,6 +241,16 @@ export class HipBackend {
     }
 
     // ------------------------------------------------ fused MoE (kind 'hip')
+    // loadExperts(path, fileOffset, blobBytes, count, arena, stride,
+    // scalesOffset, dstOffset): `count` blobs stored back to back in a pack's
+    // experts.bin streamed into the arena (blob i at dstOffset + i * stride),
+    // every fp16 scale checked finite (PackStore.readExpertBlob,
+    // src/model.js:160-167). Synchronous.
+    loadExperts(path, fileOffset, blobBytes, count, arena, stride, scalesOffset, dstOffset) {
+        this.assertAlive();
+        this.addon.loadExperts(this.ctx, String(path), fileOffset, blobBytes, count, this.owned(arena, 'arena'),
+            dstOffset || 0, stride, scalesOffset);
+    }
     moeWorkspaceBytes(tokens, width, ff, experts, topK) {
         return this.addon.moeWorkspace(tokens, width, ff, experts, topK);
     }

@@ -85,3 +85,30 @@ def test_js_host_gpu(oracle, tmp_path):
     json.dump({"cases": cases}, open(os.path.join(tmp, "manifest.json"), "w"))
     out = run_node("host_gpu.test.js", tmp)
     assert "FAIL" not in out
+
+
+def _small_pack(oracle, path, tokens):
+    W, F, E, K = 128, 64, 16, 4
+    hosts = [wl.host_layer(oracle, l, W, F, E, 11) for l in range(2)]
+    wl.write_pack(path, W, F, E, K, hosts)
+    x = np.random.default_rng(tokens).normal(0, 1, tokens * W).astype(np.float32)
+    h = hosts[1]
+    y, ids, _ = oracle.moe_layer(x, tokens, h["Wr"], h["arena"], h["stride"], h["shared"], h["Wsg"], W, F, E, K)
+    x.tofile(os.path.join(path, "x.bin"))
+    ids.astype(np.int32).tofile(os.path.join(path, "ids.bin"))
+    y.astype(np.float32).tofile(os.path.join(path, "y.bin"))
+
+
+def test_js_pack_store_cpu(oracle, tmp_path):
+    _small_pack(oracle, str(tmp_path), 1)
+    out = run_node("pack.test.js", str(tmp_path), "cpu", timeout=120)
+    assert "FAIL" not in out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tokens", [1, 29])
+def test_js_pack_store_gpu(oracle, tmp_path, tokens):
+    # The extra files (x.bin, ids.bin, y.bin) are not in the manifest's file list.
+    _small_pack(oracle, str(tmp_path), tokens)
+    out = run_node("pack.test.js", str(tmp_path), "gpu", timeout=300)
+    assert "FAIL" not in out
