@@ -359,6 +359,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack runs")
     ap.add_argument("--stack-steps", type=int, default=128)
+    ap.add_argument("--no-pack", action="store_true", help="skip the pack-loading measurement")
     ap.add_argument("--no-real", action="store_true",
                     help="skip the real model's geometry (hidden 2560, ff 640) runs")
     ap.add_argument("--no-cpu", action="store_true")
@@ -609,6 +610,32 @@ def main():
     if not args.no_real:
         real = real_model(be, wl, np, capture, replay, release)
 
+    # ---- pack loading: layer 0 written as a pack, then streamed back into HBM
+    pack = None
+    if not args.no_pack:
+        import shutil
+        import tempfile
+        d = tempfile.mkdtemp(prefix="strata-pack-")
+        try:
+            lay = layers[0]
+            host = {"arena": be.read_bytes(lay.arena), "stride": lay.stride, "shared": be.read_bytes(lay.shared),
+                    "Wr": be.read(lay.Wr), "Wsg": be.read(lay.Wsg), "gamma": be.read(lay.gamma)}
+            wl.write_pack(d, W, F, E, K, [host])
+            reader = wl.PackReader(d)
+            reader.load_layer(be, 0).free()  # page cache warm
+            t0 = time.perf_counter()
+            loaded = reader.load_layer(be, 0)
+            be.sync()
+            dt = time.perf_counter() - t0
+            same = bool(np.array_equal(be.read_bytes(loaded.arena), host["arena"]))
+            loaded.free()
+            nbytes = (E + 1) * reader.blob_bytes
+            pack = {"what": "one layer's 513 Q2 blobs from experts.bin (page cache) into the HBM arena, with the "
+                            "device scale check, plus its dense vectors", "bytes": nbytes, "seconds": round(dt, 4),
+                    "GB_per_s": round(nbytes / dt / 1e9, 2), "arena_bit_exact": same}
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -638,6 +665,7 @@ def main():
         "prefill": prefill,
         "stack": stack,
         "real_model": real,
+        "pack_load": pack,
     }
     print(json.dumps(out))
     be.dispose()
