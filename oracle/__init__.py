@@ -96,6 +96,10 @@ def lib():
             "or_ple_broadcast": (None, [_f32p, _f32p, _f32p, _i, _i]),
             "or_ple_add": (None, [_f32p, _f32p, _f32p, _i]),
             "or_argmax": (_i, [_f32p, _i]),
+            "or_bf16_project": (None, [_f32p, _u32p, _f32p, _i, _i, _i, _i, _i]),
+            "or_ple_decode": (None, [_u32p, _f32p, _i]),
+            "or_embed": (None, [_f32p, _f32p, _i, _i]),
+            "or_rope": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i]),
             "or_math_survey": (None, [_i, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                       np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")]),
         }
@@ -438,3 +442,35 @@ def ple_add(residual, gated, conv_, n):
 
 def argmax(logits, count):
     return int(lib().or_argmax(f32(logits), count))
+
+
+def bf16_project(X, codes, cols, rows, tokens, output_stride=None, output_offset=0, Y=None):
+    output_stride = rows if output_stride is None else output_stride
+    Y = np.zeros(tokens * output_stride, np.float32) if Y is None else Y
+    lib().or_bf16_project(f32(X), u32(codes), Y, cols, rows, tokens, output_stride, output_offset)
+    return Y
+
+
+def quant_gemv(X, codes, scales, offsets, cols, rows, bits, group_size, bias, codebook, has_offset):
+    """strata_quant_gemv (kernels/strata.cu:134-155): strata_quant_project's
+    arithmetic for one token, Y[row]."""
+    return quant_project(X, codes, scales, offsets, np.zeros(rows, np.float32), cols, rows, 1, rows, 0, bits,
+                         group_size, bias, codebook, has_offset)
+
+
+def ple_decode(packed_u32, count):
+    out = np.zeros(count, np.float32)
+    lib().or_ple_decode(u32(packed_u32), out, count)
+    return out
+
+
+def embed(row, width, streams):
+    out = np.zeros(width * streams, np.float32)
+    lib().or_embed(f32(row), out, width, streams)
+    return out
+
+
+def rope(X, cos, sin, dim, heads, rotary):
+    Y = np.zeros(dim * heads, np.float32)
+    lib().or_rope(f32(X), f32(cos), f32(sin), Y, dim, heads, rotary)
+    return Y

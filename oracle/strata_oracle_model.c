@@ -350,6 +350,60 @@ int or_argmax(const float *Logits, int count) {
     return id[0];
 }
 
+/* kernels/strata.cu:168-176 strata_bf16_project: bf16 weights (the high
+ * halves of f32 bit patterns, two per word) in strata_project's order. */
+void or_bf16_project(const float *X, const uint32_t *Codes, float *Y, int cols, int rows, int tokens,
+                     int outputStride, int outputOffset) {
+    for (int token = 0; token < tokens; token++)
+        for (int row = 0; row < rows; row++) {
+            float p[LANES];
+            for (int l = 0; l < LANES; l++) {
+                float sum = 0.0f;
+                for (int i = l; i < cols; i += LANES) {
+                    int ix = row * cols + i;
+                    uint32_t bits = ((Codes[ix / 2] >> ((ix % 2) * 16)) & 65535u) << 16;
+                    float w;
+                    memcpy(&w, &bits, 4);
+                    sum += w * X[token * cols + i];
+                }
+                p[l] = sum;
+            }
+            Y[token * outputStride + outputOffset + row] = tree_sum64(p);
+        }
+}
+
+float or_half_bits(uint32_t h);
+
+/* kernels/strata.cu:81-89 strata_ple_decode: IQ4_NL blocks of 18 bytes (an
+ * fp16 scale, then 16 bytes holding 32 4-bit codes: value j of the block is
+ * the low nibble of byte j (j < 16) or the high nibble of byte j - 16). */
+void or_ple_decode(const uint32_t *Packed, float *Values, int count) {
+    for (int i = 0; i < count; i++) {
+        int block = i / 32, scaleByte = block * 18, codeByte = scaleByte + 2 + i % 16;
+        uint32_t half = (Packed[scaleByte / 4] >> ((scaleByte % 4) * 8)) & 65535u;
+        int code = (int)((Packed[codeByte / 4] >> ((codeByte % 4) * 8 + (i % 32 < 16 ? 0 : 4))) & 15u);
+        Values[i] = or_half_bits(half) * iq4_value(code);
+    }
+}
+
+/* kernels/strata.cu:282-285 strata_embed: a row replicated over the streams. */
+void or_embed(const float *Row, float *Residual, int width, int streams) {
+    for (int i = 0; i < width * streams; i++) Residual[i] = Row[i % width];
+}
+
+/* kernels/strata.cu:319-327 strata_rope: NeoX half-split rotation of the
+ * first `rotary` components of each head with the given cos/sin. */
+void or_rope(const float *X, const float *Cos, const float *Sin, float *Y, int dim, int heads, int rotary) {
+    int half = rotary / 2;
+    for (int i = 0; i < dim * heads; i++) {
+        int d = i % dim, base = i - d;
+        if (d >= rotary) { Y[i] = X[i]; continue; }
+        int pair = d % half;
+        float a = X[base + pair], b = X[base + pair + half];
+        Y[i] = d < half ? a * Cos[pair] - b * Sin[pair] : b * Cos[pair] + a * Sin[pair];
+    }
+}
+
 /* ------------------------------------------------------------ self checks --- */
 /* Counts, over float bit patterns u = start, start+step, ... < end, the inputs
  * where fn (0 logf, 1 sinf, 2 cosf) differs from this platform's libm (out[0])

@@ -286,6 +286,35 @@ __global__ __launch_bounds__(64) void k_argmax(const float *Logits, int *Token, 
     if (lane == 0) Token[0] = id;
 }
 
+// kernels/strata.cu:81-89: IQ4_NL blocks of 18 bytes, an fp16 scale then 16
+// bytes of 32 codes (low nibbles first).
+__global__ void k_ple_decode(const uint32_t *Packed, float *Values, int n) {
+    int i = item();
+    if (i >= n) return;
+    int block = i / 32, scaleByte = block * 18, codeByte = scaleByte + 2 + i % 16;
+    uint32_t halfBits = (Packed[scaleByte / 4] >> ((scaleByte % 4) * 8)) & 65535u;
+    int code = (int)((Packed[codeByte / 4] >> ((codeByte % 4) * 8 + (i % 32 < 16 ? 0 : 4))) & 15u);
+    Values[i] = sm::half_bits(halfBits) * iq4_value(code);
+}
+// kernels/strata.cu:282-285
+__global__ void k_embed(const float *Row, float *Residual, int width, int n) {
+    int i = item();
+    if (i < n) Residual[i] = Row[i % width];
+}
+// kernels/strata.cu:319-327
+__global__ void k_rope(const float *X, const float *Cos, const float *Sin, float *Y, int dim, int rotary, int n) {
+    int i = item();
+    if (i >= n) return;
+    int d = i % dim, base = i - d;
+    if (d >= rotary) {
+        Y[i] = X[i];
+        return;
+    }
+    int half = rotary / 2, pair = d % half;
+    float a = X[base + pair], b = X[base + pair + half];
+    Y[i] = d < half ? a * Cos[pair] - b * Sin[pair] : b * Cos[pair] + a * Sin[pair];
+}
+
 // ------------------------------------------------------------- launchers
 int bad(sm_ctx *ctx, const std::string &m) { return fail(ctx, SM_E_ARG, m); }
 unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -540,6 +569,42 @@ int L_argmax(sm_ctx *ctx, const uint32_t *G, Args a) {
     return launched(ctx);
 }
 
+int L_ple_decode(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int count = a.i32(2);
+    int64_t plen = buf_len(ctx, a.ptr(0)), vlen = buf_len(ctx, a.ptr(1));
+    if (count < 1) return bad(ctx, "strata_ple_decode.count must be an integer in [1, 2147483647]");
+    if (count % 32 || (plen >= 0 && ((int64_t)count / 32 * 18 + 3) / 4 * 4 > plen) || (vlen >= 0 && count * 4LL > vlen))
+        return fail(ctx, SM_E_ARG, "Invalid packed PLE layout");
+    int64_t n = covered(G, count);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)(((n - 1) / 32 * 18 + 18 + 3) / 4 * 4), "Packed")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "Values")) return rc;
+    k_ple_decode<<<blocks256(n), 256, 0, ctx->stream>>>((const uint32_t *)a.ptr(0), Fw(a, 1), (int)n);
+    return launched(ctx);
+}
+
+int L_embed(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(2), streams = a.i32(3);
+    if (width < 1 || streams < 1) return bad(ctx, "strata_embed: width and streams must be >= 1");
+    int64_t n = covered(G, (int64_t)width * streams);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)std::min<int64_t>(n, width) * 4, "Row")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "Residual")) return rc;
+    k_embed<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), Fw(a, 1), width, (int)n);
+    return launched(ctx);
+}
+
+int L_rope(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(4), heads = a.i32(5), rotary = a.i32(6);
+    if (dim < 1 || heads < 1 || rotary < 1) return bad(ctx, "strata_rope: dim, heads, rotary must be >= 1");
+    if (rotary % 2 || rotary > dim) return bad(ctx, "Rotary width must be even and <= head dimension");
+    int64_t n = covered(G, (int64_t)dim * heads);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)((n - 1) / dim + 1) * dim * 4, "X")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)(rotary / 2) * 4, "Cos")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)(rotary / 2) * 4, "Sin")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)n * 4, "Y")) return rc;
+    k_rope<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3), dim, rotary, (int)n);
+    return launched(ctx);
+}
+
 // Parameter lists in the reference's order (kernels/strata.cu).
 const Entry kModelEntries[] = {
     {"strata_embedding",
@@ -567,6 +632,9 @@ const Entry kModelEntries[] = {
     {"strata_ple_broadcast", "Value:f32*,Gate:f32*,Y:f32*,width:i32,streams:i32", 5, L_ple_broadcast},
     {"strata_ple_add", "Residual:f32*,Gated:f32*,Conv:f32*,n:i32", 4, L_ple_add},
     {"strata_argmax", "Logits:f32*,Token:i32*,count:i32", 3, L_argmax},
+    {"strata_ple_decode", "Packed:u32*,Values:f32*,count:i32", 3, L_ple_decode},
+    {"strata_embed", "Row:f32*,Residual:f32*,width:i32,streams:i32", 4, L_embed},
+    {"strata_rope", "X:f32*,Cos:f32*,Sin:f32*,Y:f32*,dim:i32,heads:i32,rotary:i32", 7, L_rope},
 };
 
 }  // namespace

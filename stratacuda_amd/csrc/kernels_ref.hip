@@ -64,6 +64,24 @@ __global__ void k_project(const float *X, const float *W, float *Y, int cols, in
     if (lane == 0) Y[(int64_t)token * outputStride + outputOffset + row] = sum;
 }
 
+// kernels/strata.cu:168-176 strata_bf16_project: bf16 weights, two per word
+// (element ix in the half ix % 2 of word ix / 2), widened exactly to f32.
+__global__ void k_bf16_project(const float *X, const uint32_t *Codes, float *Y, int cols, int rows, int tokens,
+                               int outputStride, int outputOffset, uint32_t gx, uint64_t total) {
+    uint64_t g;
+    if (!logical_group(total, g)) return;
+    int row = (int)(g % gx), token = (int)(g / gx), lane = lane_id();
+    if (row >= rows || token >= tokens) return;
+    const float *x = X + (int64_t)token * cols;
+    float sum = 0.0f;
+    for (int i = lane; i < cols; i += 64) {
+        const int64_t ix = (int64_t)row * cols + i;
+        sum = sum + __uint_as_float(((Codes[ix / 2] >> ((ix % 2) * 16)) & 65535u) << 16) * x[i];
+    }
+    sum = sm::tree_sum64(sum);
+    if (lane == 0) Y[(int64_t)token * outputStride + outputOffset + row] = sum;
+}
+
 // kernels/strata.cu:38-55 strata_q2_gate_up
 __global__ void k_q2_gate_up(const float *X, const uint32_t *Blob, const float *Scales, const int *Mapping,
                              float *Hidden, int width, int ff, int tokens, int mapped, int expanded, int codeOffset,
@@ -453,6 +471,41 @@ int L_quant_project(sm_ctx *ctx, const uint32_t *G, Args a) {
     return launched(ctx);
 }
 
+int L_bf16_project(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int cols = a.i32(3), rows = a.i32(4), tokens = a.i32(5), stride = a.i32(6), off = a.i32(7), rr, tt;
+    if (int rc = projection_layout(ctx, "strata_bf16_project", a.ptr(0), a.ptr(2), cols, rows, tokens, stride, off,
+                                   &rr, &tt, G))
+        return rc;
+    if (int rc = need(ctx, a.ptr(1), ((uint64_t)rr * cols + 1) / 2 * 4, "strata_bf16_project.Codes")) return rc;
+    uint64_t total = (uint64_t)G[0] * G[1];
+    k_bf16_project<<<blocks_for(total), 256, 0, ctx->stream>>>((const float *)a.ptr(0), (const uint32_t *)a.ptr(1),
+                                                               (float *)a.ptr(2), cols, rows, tokens, stride, off,
+                                                               G[0], total);
+    return launched(ctx);
+}
+
+// kernels/strata.cu:134-155 strata_quant_gemv: strata_quant_project's
+// arithmetic for one token, grid [rows, 1, 1].
+int L_quant_gemv(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int cols = a.i32(5), rows = a.i32(6), bits = a.i32(7), groupSize = a.i32(8), bias = a.i32(9);
+    int codebook = a.i32(10), hasOffset = a.i32(11), rr, tt;
+    if (bits != 2 && bits != 4 && bits != 8) return bad(ctx, "Canonical code width must be 2, 4 or 8");
+    if (groupSize < 1 || cols % groupSize || (int64_t)cols * rows * bits > 0x7fffffff)
+        return bad(ctx, "Quantized rows must contain whole groups and fit 31-bit indexing");
+    const uint32_t G1[3] = {G[0], 1, 1};
+    if (int rc = projection_layout(ctx, "strata_quant_gemv", a.ptr(0), a.ptr(4), cols, rows, 1, rows, 0, &rr, &tt, G1))
+        return rc;
+    uint64_t elems = (uint64_t)rr * cols;
+    if (int rc = need(ctx, a.ptr(1), (elems * bits + 31) / 32 * 4, "Codes")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (elems / groupSize) * 4, "Scales")) return rc;
+    if (hasOffset)
+        if (int rc = need(ctx, a.ptr(3), (elems / groupSize) * 4, "Offsets")) return rc;
+    k_quant_project<<<blocks_for(G[0]), 256, 0, ctx->stream>>>(
+        (const float *)a.ptr(0), (const uint32_t *)a.ptr(1), (const float *)a.ptr(2), (const float *)a.ptr(3),
+        (float *)a.ptr(4), cols, rows, 1, rows, 0, bits, groupSize, bias, codebook, hasOffset, G[0], G[0]);
+    return launched(ctx);
+}
+
 int L_norm(sm_ctx *ctx, const uint32_t *G, Args a) {
     int cols = a.i32(3), rows = a.i32(4), weightRows = a.i32(5), mode = a.i32(6);
     float eps = a.f32(7), scale = a.f32(8);
@@ -569,6 +622,12 @@ const Entry kEntries[] = {
      "X:f32*,Codes:u32*,Scales:f32*,Offsets:f32*,Y:f32*,cols:i32,rows:i32,tokens:i32,outputStride:i32,"
      "outputOffset:i32,bits:i32,groupSize:i32,bias:i32,codebook:i32,hasOffset:i32",
      15, L_quant_project},
+    {"strata_bf16_project",
+     "X:f32*,Codes:u32*,Y:f32*,cols:i32,rows:i32,tokens:i32,outputStride:i32,outputOffset:i32", 8, L_bf16_project},
+    {"strata_quant_gemv",
+     "X:f32*,Codes:u32*,Scales:f32*,Offsets:f32*,Y:f32*,cols:i32,rows:i32,bits:i32,groupSize:i32,bias:i32,"
+     "codebook:i32,hasOffset:i32",
+     12, L_quant_gemv},
     {"strata_norm", "X:f32*,W:f32*,Y:f32*,cols:i32,rows:i32,weightRows:i32,mode:i32,epsilon:f32,scale:f32", 9, L_norm},
     {"strata_elementwise", "A:f32*,B:f32*,Y:f32*,n:i32,mode:i32,scale:f32", 6, L_elementwise},
     {"strata_router", "Logits:f32*,Ids:i32*,Weights:f32*,experts:i32,topK:i32", 5, L_router},

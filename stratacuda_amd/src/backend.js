@@ -32,8 +32,7 @@ export function requireInteger(n, label, min = 1, max = 0x7fffffff) {
 }
 
 // Argument checks run before any launch, with the reference's conditions and
-// messages (src/backend.js:10-56) for the kernels this library provides
-// (strata_ple_decode and the batched prompt kernels are not among them).
+// messages (src/backend.js:10-56) for the kernels this library provides.
 const PROJECTIONS = ['strata_project', 'strata_quant_project', 'strata_bf16_project', 'strata_q2_project'];
 export function validateDispatch(name, args) {
     const get = k => requireInteger(args[k], name + '.' + k);
@@ -82,6 +81,11 @@ export function validateDispatch(name, args) {
     }
     if (name === 'strata_rope_frequencies' && (!Number.isFinite(args.base) || args.base <= 1 || get('rotary') % 2))
         throw Error('Invalid RoPE frequencies');
+    if (name === 'strata_ple_decode' && (get('count') % 32 || Math.ceil(args.count / 32 * 18 / 4) > args.Packed.length ||
+        args.count > args.Values.length))
+        throw Error('Invalid packed PLE layout');
+    if (name === 'strata_rope' && (get('rotary') % 2 || args.rotary > get('dim')))
+        throw new RangeError('Rotary width must be even and <= head dimension');
     if (name === 'strata_attention') {
         if (get('heads') % get('kvHeads')) throw new RangeError('Attention heads must be divisible by KV heads');
         requireInteger(args.count, 'attention selected cells', 1, 2048);

@@ -230,3 +230,58 @@ def test_invalid_layouts_are_rejected(backend):
                                     "Y": backend.alloc(7), "channels": 7, "taps": 4, "dilation": 3, "activation": 1},
                     [1, 1, 1])
     assert e.value.code == -3
+
+
+def test_bf16_project_quant_gemv_ple_decode_embed_rope(backend, oracle):
+    rng = np.random.default_rng(21)
+    # bf16 projection with a strided, offset batch output
+    cols, rows, tokens, stride, off = 2560, 37, 3, 45, 4
+    w = rng.normal(0, 0.05, rows * cols).astype(np.float32)
+    hi = (w.view(np.uint32) >> 16).astype(np.uint32)
+    codes = (hi[0::2] | (hi[1::2] << 16)).astype(np.uint32)
+    x = rng.normal(0, 1, tokens * cols).astype(np.float32)
+    y = backend.alloc(np.full(tokens * stride, -3, np.float32))
+    backend.run("strata_bf16_project", {"X": backend.alloc(x), "Codes": backend.alloc(codes, "u32"), "Y": y,
+                                        "cols": cols, "rows": rows, "tokens": tokens, "outputStride": stride,
+                                        "outputOffset": off}, [rows, tokens, 1])
+    same(backend.read(y), oracle.bf16_project(x, codes, cols, rows, tokens, stride, off,
+                                              Y=np.full(tokens * stride, -3, np.float32)))
+    # S2 / S4 / S8 GEMV (tests/conformance.js:40-44 recipe)
+    for bits in (2, 4, 8):
+        cols, rows, gs, mask = 64, 5, 16, (1 << bits) - 1
+        cw = np.zeros((cols * rows * bits + 31) // 32, np.uint32)
+        for i in range(cols * rows):
+            cw[(i * bits) >> 5] |= np.uint32(((i * 13 + 7) & mask) << ((i * bits) & 31))
+        sc = ((np.arange(cols * rows // gs) % 7 - 3) * 0.03).astype(np.float32)
+        of = (np.arange(cols * rows // gs) * 0.001).astype(np.float32)
+        xv = np.sin(np.arange(cols)).astype(np.float32)
+        out = backend.alloc(rows)
+        backend.run("strata_quant_gemv", {"X": backend.alloc(xv), "Codes": backend.alloc(cw, "u32"),
+                                          "Scales": backend.alloc(sc), "Offsets": backend.alloc(of), "Y": out,
+                                          "cols": cols, "rows": rows, "bits": bits, "groupSize": gs, "bias": -3,
+                                          "codebook": 0, "hasOffset": 1}, [rows, 1, 1])
+        same(backend.read(out), oracle.quant_gemv(xv, cw, sc, of, cols, rows, bits, gs, -3, 0, 1))
+    # IQ4_NL PLE rows: 2560 values (80 blocks of 18 bytes)
+    raw = rng.integers(0, 256, 80 * 18 + 2, dtype=np.uint8)
+    for b in range(80):
+        raw[b * 18:b * 18 + 2] = np.frombuffer(np.float16(rng.normal(0, 0.02)).tobytes(), np.uint8)
+    packed = np.frombuffer(raw.tobytes(), np.uint32).copy()
+    vals = backend.alloc(2560)
+    backend.run("strata_ple_decode", {"Packed": backend.alloc(packed, "u32"), "Values": vals, "count": 2560},
+                grid(2560))
+    same(backend.read(vals), oracle.ple_decode(packed, 2560))
+    # row broadcast and rotation with supplied cos / sin
+    row = rng.normal(0, 1, 64).astype(np.float32)
+    res = backend.alloc(256)
+    backend.run("strata_embed", {"Row": backend.alloc(row), "Residual": res, "width": 64, "streams": 4}, grid(256))
+    same(backend.read(res), oracle.embed(row, 64, 4))
+    xr = np.sin(np.arange(24)).astype(np.float32)
+    c = np.cos(13 / 10000 ** (np.arange(2) / 2)).astype(np.float32)
+    s = np.sin(13 / 10000 ** (np.arange(2) / 2)).astype(np.float32)
+    yr = backend.alloc(24)
+    backend.run("strata_rope", {"X": backend.alloc(xr), "Cos": backend.alloc(c), "Sin": backend.alloc(s), "Y": yr,
+                                "dim": 8, "heads": 3, "rotary": 4}, [1, 1, 1])
+    same(backend.read(yr), oracle.rope(xr, c, s, 8, 3, 4))
+    with pytest.raises(sm.StrataError):  # count not a whole number of blocks
+        backend.run("strata_ple_decode", {"Packed": backend.alloc(packed, "u32"), "Values": vals, "count": 100},
+                    grid(100))

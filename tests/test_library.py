@@ -50,7 +50,8 @@ def test_kernel_table_lists_reference_kernels():
                  "strata_embedding", "strata_rope_frequencies", "strata_rope_table", "strata_rope_position",
                  "strata_hc_mix", "strata_hc_write", "strata_conv", "strata_gdn_gates", "strata_gdn_step",
                  "strata_slice", "strata_kv_append", "strata_attention", "strata_attention_gate", "strata_ple_gate",
-                 "strata_ple_broadcast", "strata_ple_add", "strata_argmax"]:
+                 "strata_ple_broadcast", "strata_ple_add", "strata_argmax", "strata_bf16_project",
+                 "strata_quant_gemv", "strata_ple_decode", "strata_embed", "strata_rope"]:
         assert name in sigs, name
 
 

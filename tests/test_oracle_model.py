@@ -256,3 +256,64 @@ def test_embedding_formats(oracle):
                      has_offset=1)
     want = ((c4 - 8) * sc[np.arange(W) // 16]).astype(np.float32) + off[np.arange(W) // 16]
     assert np.array_equal(res, want.astype(np.float32))
+
+
+def test_bf16_projection_is_lossless_compact_f32(oracle):
+    # tests/conformance.js:101-107 "Lossless compact BF16 projections": f32
+    # weights whose low 16 bits are zero project bit-identically from their
+    # bf16 halves.
+    rng = np.random.default_rng(11)
+    cols, rows, tokens = 2560, 37, 3
+    w = (rng.normal(0, 0.05, rows * cols).astype(np.float32).view(np.uint32) & 0xFFFF0000).view(np.float32)
+    x = rng.normal(0, 1, tokens * cols).astype(np.float32)
+    hi = (w.view(np.uint32) >> 16).astype(np.uint32)
+    codes = (hi[0::2] | (hi[1::2] << 16)).astype(np.uint32)
+    got = oracle.bf16_project(x, codes, cols, rows, tokens, rows + 5, 2)
+    want = oracle.project(x, w, cols, rows, tokens, rows + 5, 2)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quant_gemv_kat(oracle, bits):
+    # tests/conformance.js:40-44: cols 64, rows 5, group 16, bias -3, signed
+    # scales (i % 7 - 3) * 0.03, offsets i * 0.001, codes (i * 13 + 7) & mask.
+    cols, rows, gs, mask = 64, 5, 16, (1 << bits) - 1
+    codes = np.zeros((cols * rows * bits + 31) // 32, np.uint32)
+    for i in range(cols * rows):
+        bit = i * bits
+        codes[bit >> 5] |= np.uint32(((i * 13 + 7) & mask) << (bit & 31))
+    scales = ((np.arange(cols * rows // gs) % 7 - 3) * 0.03).astype(np.float32)
+    offsets = (np.arange(cols * rows // gs) * 0.001).astype(np.float32)
+    x = np.sin(np.arange(cols)).astype(np.float32)
+    i = np.arange(rows * cols)
+    wv = (((i * 13 + 7) & mask) - 3) * scales[i // gs].astype(np.float64) + offsets[i // gs]
+    ref = wv.reshape(rows, cols) @ x.astype(np.float64)
+    ref_compare(oracle.quant_gemv(x, codes, scales, offsets, cols, rows, bits, gs, -3, 0, 1), ref)
+
+
+def test_ple_decode_iq4nl_blocks(oracle):
+    # IQ4_NL blocks (18 bytes: fp16 scale + 16 bytes of 32 nibbles, low
+    # nibbles first) at unaligned 18-byte strides with signed scales.
+    rng = np.random.default_rng(3)
+    blocks = 37
+    raw = np.zeros(blocks * 18 + 2, np.uint8)
+    scales = (rng.normal(0, 0.02, blocks)).astype(np.float16)
+    nib = rng.integers(0, 16, (blocks, 32))
+    for b in range(blocks):
+        raw[b * 18:b * 18 + 2] = np.frombuffer(scales[b].tobytes(), np.uint8)
+        raw[b * 18 + 2:b * 18 + 18] = (nib[b, :16] | (nib[b, 16:] << 4)).astype(np.uint8)
+    packed = np.frombuffer(raw.tobytes(), np.uint32)
+    iq4 = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+    want = (scales.astype(np.float32)[:, None] * iq4[nib]).reshape(-1)
+    got = oracle.ple_decode(packed, blocks * 32)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+def test_partial_neox_rope_kat(oracle):
+    # tests/conformance.js:67-68: x = sin(i) (24 values: 3 heads of 8), rotary
+    # 4, cos/sin of 13 / 10000^(i/2), against pos 13, base 10000.
+    x = np.sin(np.arange(24)).astype(np.float32)
+    c = np.cos(13 / 10000 ** (np.arange(2) / 2)).astype(np.float32)
+    s = np.sin(13 / 10000 ** (np.arange(2) / 2)).astype(np.float32)
+    ref_compare(oracle.rope(x, c, s, 8, 3, 4), f64.rope(x.astype(np.float64), 8, 4, 13, 10000))
+    assert np.array_equal(oracle.embed(x[:8], 8, 3), np.tile(x[:8], 3))
