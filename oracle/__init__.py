@@ -97,6 +97,17 @@ def lib():
             "or_ple_add": (None, [_f32p, _f32p, _f32p, _i]),
             "or_argmax": (_i, [_f32p, _i]),
             "or_bf16_project": (None, [_f32p, _u32p, _f32p, _i, _i, _i, _i, _i]),
+            "or_embed_batch": (None, [_f32p, _f32p, _i, _i, _i]),
+            "or_hc_mix_batch": (None, [_f32p, _f32p, _f32p, _i, _i, _i]),
+            "or_hc_write_batch": (None, [_f32p, _f32p, _f32p, _i, _i, _i]),
+            "or_conv_batch": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _i]),
+            "or_gdn_gates_batch": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i, _i]),
+            "or_gdn_batch": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i]),
+            "or_rope_batch": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i]),
+            "or_kv_append_batch": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i]),
+            "or_attention_gate_batch": (None, [_f32p, _f32p, _f32p, _i, _i, _i]),
+            "or_ple_broadcast_batch": (None, [_f32p, _f32p, _f32p, _i, _i, _i]),
+            "or_attention_batch": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, ctypes.c_float, _i]),
             "or_ple_decode": (None, [_u32p, _f32p, _i]),
             "or_embed": (None, [_f32p, _f32p, _i, _i]),
             "or_rope": (None, [_f32p, _f32p, _f32p, _f32p, _i, _i, _i]),
@@ -473,4 +484,69 @@ def embed(row, width, streams):
 def rope(X, cos, sin, dim, heads, rotary):
     Y = np.zeros(dim * heads, np.float32)
     lib().or_rope(f32(X), f32(cos), f32(sin), Y, dim, heads, rotary)
+    return Y
+
+
+# ------------------------------------------------ prompt (batch) kernels
+def embed_batch(rows, width, streams, tokens):
+    out = np.zeros(width * streams * tokens, np.float32)
+    lib().or_embed_batch(f32(rows), out, width, streams, tokens)
+    return out
+
+
+def hc_mix_batch(norm_, gate, width, streams, tokens):
+    out = np.zeros(width * tokens, np.float32)
+    lib().or_hc_mix_batch(f32(norm_), f32(gate), out, width, streams, tokens)
+    return out
+
+
+def hc_write_batch(residual, output, inject, width, streams, tokens):
+    lib().or_hc_write_batch(residual, f32(output), f32(inject), width, streams, tokens)
+    return residual
+
+
+def conv_batch(history, X, W, channels, taps, dilation, activation, tokens):
+    Y = np.zeros(channels * tokens, np.float32)
+    lib().or_conv_batch(history, f32(X), f32(W), Y, channels, taps, dilation, activation, tokens)
+    return Y
+
+
+def gdn_gates_batch(alpha, beta, A, dt, heads, tokens):
+    decay, strength = np.zeros(heads * tokens, np.float32), np.zeros(heads * tokens, np.float32)
+    lib().or_gdn_gates_batch(f32(alpha), f32(beta), f32(A), f32(dt), decay, strength, heads, tokens)
+    return decay, strength
+
+
+def gdn_batch(state, q, k, v, decay, beta, dim, key_heads, value_heads, tokens):
+    Y = np.zeros(dim * value_heads * tokens, np.float32)
+    lib().or_gdn_batch(state, f32(q), f32(k), f32(v), f32(decay), f32(beta), Y, dim, key_heads, value_heads, tokens)
+    return Y
+
+
+def rope_batch(X, cos, sin, dim, heads, rotary, tokens):
+    Y = np.zeros(dim * heads * tokens, np.float32)
+    lib().or_rope_batch(f32(X), f32(cos), f32(sin), Y, dim, heads, rotary, tokens)
+    return Y
+
+
+def kv_append_batch(k, v, keys, values, width, position, tokens):
+    lib().or_kv_append_batch(f32(k), f32(v), keys, values, width, position, tokens)
+
+
+def attention_gate_batch(attn, full_q, dim, heads, tokens):
+    Y = np.zeros(dim * heads * tokens, np.float32)
+    lib().or_attention_gate_batch(f32(attn), f32(full_q), Y, dim, heads, tokens)
+    return Y
+
+
+def ple_broadcast_batch(value, gate, width, streams, tokens):
+    Y = np.zeros(width * streams * tokens, np.float32)
+    lib().or_ple_broadcast_batch(f32(value), f32(gate), Y, width, streams, tokens)
+    return Y
+
+
+def attention_batch(Q, keys, values, dim, heads, kv_heads, position, scale, tokens):
+    Y = np.zeros(dim * heads * tokens, np.float32)
+    lib().or_attention_batch(f32(Q), f32(keys), f32(values), Y, dim, heads, kv_heads, position,
+                             float(np.float32(scale)), tokens)
     return Y

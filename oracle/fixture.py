@@ -19,9 +19,11 @@ import math
 
 import numpy as np
 
-from . import (argmax, attention, attention_gate, conv, elementwise, embedding, gdn_gates, gdn_step, hc_mix, hc_write,
-               kv_append, moe_combine, norm, ple_add, ple_broadcast, ple_gate, project, rope_frequencies,
-               rope_position, rope_table, router, slice_)
+from . import (argmax, attention, attention_batch, attention_gate, attention_gate_batch, conv, conv_batch, elementwise,
+               embedding, gather_rows, gdn_batch, gdn_gates, gdn_gates_batch, gdn_step, hc_mix, hc_mix_batch, hc_write,
+               hc_write_batch, kv_append, kv_append_batch, moe_combine, norm, ple_add, ple_broadcast,
+               ple_broadcast_batch, ple_gate, project, rope_frequencies, rope_position, rope_table, router,
+               scatter_rows, slice_)
 
 # src/fixture.js:4-6
 GEOMETRY = dict(width=32, streams=2, rank=8, layers=4, qsaInterval=4, ssmDim=8, keyHeads=2, valueHeads=4, heads=4,
@@ -284,3 +286,153 @@ class OracleEngine:
             self.previous.pop(0)
         self.position += 1
         return token_out, logits
+
+
+class OraclePromptBatch:
+    """PromptBatch (src/prefill.js:5-97): one chunk of prompt tokens through
+    every layer, layer-major, with the batched kernels and per-expert row
+    groups, on an OracleEngine's state."""
+
+    def __init__(self, engine, tokens):
+        self.e, self.g, self.tokens, self.n = engine, engine.g, list(tokens), len(tokens)
+        self.position = engine.position
+
+    def mat(self, name, x):
+        shape = self.e.f.shape(name)
+        cols, rows = shape[0], int(np.prod(shape[1:]))
+        return project(x, self.e.f.data(name), cols, rows, self.n)
+
+    def hc(self, prefix, inject=True):
+        g, n = self.g, self.n
+        nm = norm(self.residual, self.e.vec(prefix + "norm.weight"), g["width"], n * g["streams"], g["streams"])
+        down = self.mat(prefix + "down.weight", nm)
+        lo = elementwise(down, down, 1, np.float32(1 / g["streams"]))
+        gate = self.mat(prefix + "up.weight", lo)
+        mixed = hc_mix_batch(nm, gate, g["width"], g["streams"], n)
+        return mixed, (self.mat(prefix + "inject.weight", nm) if inject else None)
+
+    def write(self, output, inject):
+        hc_write_batch(self.residual, output, inject, self.g["width"], self.g["streams"], self.n)
+
+    def ple(self):
+        g, n, e = self.g, self.n, self.e
+        p, hc = "blk.%d.ple_" % g["pleLayer"], g["width"] * g["streams"]
+        previous, rows = list(e.previous), []
+        table, hd = e.f.data("per_layer_token_embd.weight"), g["pleHeadDim"]
+        for t in self.tokens:
+            r = ngram_rows(t, previous, e.f.constants, g["eos"])
+            rows.append(np.concatenate([table[i * hd:(i + 1) * hd] for i in r]))
+            previous.append(t)
+            if len(previous) > 2:
+                previous.pop(0)
+        emb = np.concatenate(rows).astype(np.float32)
+        key = norm(self.mat(p + "key.weight", emb), e.vec(p + "norm_key.weight"), g["width"], n * g["streams"],
+                   g["streams"])
+        query = norm(self.residual, e.vec(p + "norm_query.weight"), g["width"], n * g["streams"], g["streams"])
+        value = self.mat(p + "value.weight", emb)
+        gate = ple_gate(key, query, g["width"], n * g["streams"])
+        gated = ple_broadcast_batch(value, gate, g["width"], g["streams"], n)
+        nm = norm(gated, e.vec(p + "norm_conv.weight"), g["width"], n * g["streams"], g["streams"])
+        cv = conv_batch(e.ple_history, nm, e.vec(p + "conv1d.weight"), hc, g["pleTaps"], g["pleDilation"], 1, n)
+        ple_add(self.residual, gated, cv, n * hc)
+
+    def gdn(self, layer, x):
+        g, n, e = self.g, self.n, self.e
+        p, st = "blk.%d." % layer, e.states[layer]
+        qk, vn = g["ssmDim"] * g["keyHeads"], g["ssmDim"] * g["valueHeads"]
+        c = 2 * qk + vn
+        qkv = self.mat(p + "attn_qkv.weight", x)
+        cv = conv_batch(st["conv"], qkv, e.vec(p + "ssm_conv1d.weight"), c, 4, 1, 1, n)
+        qr, kr, v = slice_(cv, qk, n, c), slice_(cv, qk, n, c, qk), slice_(cv, vn, n, c, 2 * qk)
+        q = norm(qr, qr, g["ssmDim"], n * g["keyHeads"], 1, 1, 1e-6, np.float32(1 / math.sqrt(g["ssmDim"])))
+        k = norm(kr, kr, g["ssmDim"], n * g["keyHeads"], 1, 1)
+        alpha, beta = self.mat(p + "ssm_alpha.weight", x), self.mat(p + "ssm_beta.weight", x)
+        decay, strength = gdn_gates_batch(alpha, beta, e.vec(p + "ssm_a"), e.vec(p + "ssm_dt.bias"), g["valueHeads"], n)
+        y = gdn_batch(st["state"], q, k, v, decay, strength, g["ssmDim"], g["keyHeads"], g["valueHeads"], n)
+        z = self.mat(p + "attn_gate.weight", x)
+        nm = norm(y, e.vec(p + "ssm_norm.weight"), g["ssmDim"], n * g["valueHeads"])
+        return self.mat(p + "ssm_out.weight", elementwise(nm, z, 4))
+
+    def rotate(self, x, heads):
+        g, e = self.g, self.e
+        if e.rope is None:
+            hi, lo = rope_frequencies(g["rotary"], g["ropeBase"])
+            e.rope = rope_table(hi, lo, g["rotary"], g["context"])
+        return rope_position(x, e.rope[0], e.rope[1], g["headDim"], heads, g["rotary"], self.position, self.n)
+
+    def qsa(self, layer, x):
+        g, n, e = self.g, self.n, self.e
+        p, st, hd = "blk.%d." % layer, e.states[layer], g["headDim"]
+        full = self.mat(p + "attn_q.weight", x)
+        qr = slice_(full, hd, n * g["heads"], hd * 2)
+        q = self.rotate(norm(qr, e.vec(p + "attn_q_norm.weight"), hd, n * g["heads"]), g["heads"])
+        kr = self.mat(p + "attn_k.weight", x)
+        k = self.rotate(norm(kr, e.vec(p + "attn_k_norm.weight"), hd, n * g["kvHeads"]), g["kvHeads"])
+        v = self.mat(p + "attn_v.weight", x)
+        kv_append_batch(k, v, st["keys"], st["values"], g["kvHeads"] * hd, self.position, n)
+        attn = attention_batch(q, st["keys"], st["values"], hd, g["heads"], g["kvHeads"], self.position,
+                               np.float32(1 / math.sqrt(hd)), n)
+        return self.mat(p + "attn_output.weight", attention_gate_batch(attn, full, hd, g["heads"], n))
+
+    def expert(self, prefix, x, tokens, shared=False):
+        name = (lambda r: prefix + "ffn_" + r + "_shexp.weight") if shared else (lambda r: prefix + r)
+
+        def m(nm, v):
+            shape = self.e.f.shape(nm)
+            return project(v, self.e.f.data(nm), shape[0], int(np.prod(shape[1:])), tokens)
+        return m(name("down"), elementwise(m(name("gate"), x), m(name("up"), x), 3))
+
+    def moe(self, layer, x):
+        g, n, e = self.g, self.n, self.e
+        p, K, W = "blk.%d." % layer, g["topK"], g["width"]
+        logits = self.mat(p + "ffn_gate_inp.weight", x)
+        ids, weights = router(logits, g["experts"], K, n)
+        groups = {}
+        for t in range(n):
+            row = [int(i) for i in ids[t * K:(t + 1) * K]]
+            if any(i < 0 or i >= g["experts"] for i in row) or len(set(row)) != K:
+                raise RuntimeError("Invalid prompt expert routing")
+            e.routes.append({"position": self.position + t, "layer": layer, "ids": row})
+            for k, i in enumerate(row):
+                groups.setdefault(i, []).append((t, t * K + k))
+        parts = np.zeros(n * K * W, np.float32)
+        for i, jobs in groups.items():
+            inp = gather_rows(x, np.array([j[0] for j in jobs], np.int32), W, len(jobs))
+            out = self.expert(p + "expert.%d." % i, inp, len(jobs))
+            scatter_rows(out, np.array([j[1] for j in jobs], np.int32), parts, W, len(jobs))
+        shared = self.expert(p, x, n, True)
+        shared_gate = self.mat(p + "ffn_gate_inp_shexp.weight", x)
+        return moe_combine(parts, weights, shared, shared_gate, W, K, n)
+
+    def run(self):
+        g, n, e = self.g, self.n, self.e
+        hc = g["width"] * g["streams"]
+        self.residual = np.zeros(n * hc, np.float32)
+        emb, w = e.f.data("token_embd.weight"), g["width"]
+        for t, tok in enumerate(self.tokens):
+            self.residual[t * hc:(t + 1) * hc] = np.tile(emb[tok * w:(tok + 1) * w], g["streams"])
+        for l in range(g["layers"]):
+            if l == g["pleLayer"]:
+                self.ple()
+            mixed, inject = self.hc("blk.%d.hc_attn_" % l)
+            out = self.qsa(l, mixed) if l % g["qsaInterval"] == g["qsaInterval"] - 1 else self.gdn(l, mixed)
+            self.write(out, inject)
+            mixed, inject = self.hc("blk.%d.hc_ffn_" % l)
+            self.write(self.moe(l, mixed), inject)
+        e.residual[:] = self.residual[(n - 1) * hc:]
+        e.position += n
+        e.previous = (e.previous + self.tokens)[-2:]
+
+
+def prefill(engine, tokens, chunk_size=16, predict=True):
+    """prefillChunks (src/prefill.js:99-111): chunks of the prompt through
+    OraclePromptBatch, then the head on the last token's residual."""
+    engine.routes = []
+    tokens = list(tokens)
+    for off in range(0, len(tokens), chunk_size):
+        OraclePromptBatch(engine, tokens[off:off + chunk_size]).run()
+    if not predict:
+        return None, None
+    head, _ = engine.hc("output_hc_", False)
+    logits = engine.mat("output.weight", head)
+    return argmax(logits, engine.g["vocab"]), logits

@@ -404,6 +404,150 @@ void or_rope(const float *X, const float *Cos, const float *Sin, float *Y, int d
     }
 }
 
+/* ------------------------------------------------- prompt (batch) kernels --- */
+/* kernels/strata.cu:399-402 strata_embed_batch: token t's row over the streams. */
+void or_embed_batch(const float *Rows, float *Residual, int width, int streams, int tokens) {
+    int hc = width * streams;
+    for (int i = 0; i < hc * tokens; i++) Residual[i] = Rows[(i / hc) * width + i % width];
+}
+/* kernels/strata.cu:403-408 strata_hc_mix_batch */
+void or_hc_mix_batch(const float *Norm, const float *Gate, float *Mixed, int width, int streams, int tokens) {
+    for (int i = 0; i < width * tokens; i++) {
+        int token = i / width, d = i % width;
+        float v = 0.0f;
+        for (int c = 0; c < streams; ++c) {
+            int p = (token * streams + c) * width + d;
+            v += Norm[p] * or_sigmoid(Gate[p]);
+        }
+        Mixed[i] = v / (float)streams;
+    }
+}
+/* kernels/strata.cu:409-412 strata_hc_write_batch */
+void or_hc_write_batch(float *Residual, const float *Output, const float *Inject, int width, int streams, int tokens) {
+    int hc = width * streams;
+    for (int i = 0; i < hc * tokens; i++)
+        Residual[i] += Output[(i / hc) * width + i % width] * (2.0f * or_sigmoid(Inject[i / width] / (float)streams));
+}
+/* kernels/strata.cu:413-424 strata_conv_batch: each channel's tokens in order. */
+void or_conv_batch(float *History, const float *X, const float *W, float *Y, int channels, int taps, int dilation,
+                   int activation, int tokens) {
+    int span = (taps - 1) * dilation;
+    for (int c = 0; c < channels; c++) {
+        float *h = History + (int64_t)c * span;
+        for (int token = 0; token < tokens; ++token) {
+            float sum = 0.0f;
+            for (int t = 0; t < taps - 1; ++t) sum += h[t * dilation] * W[c * taps + t];
+            sum += X[token * channels + c] * W[c * taps + taps - 1];
+            Y[token * channels + c] = activation == 1 ? or_silu(sum) : sum;
+            for (int t = 0; t < span - 1; ++t) h[t] = h[t + 1];
+            if (span > 0) h[span - 1] = X[token * channels + c];
+        }
+    }
+}
+/* kernels/strata.cu:425-431 strata_gdn_gates_batch */
+void or_gdn_gates_batch(const float *Alpha, const float *Beta, const float *A, const float *Dt, float *Decay,
+                        float *Strength, int heads, int tokens) {
+    for (int i = 0; i < heads * tokens; i++) {
+        float x = Alpha[i] + Dt[i % heads];
+        float sp = x > 20.0f ? x : or_logf(1.0f + or_expf(x));
+        Decay[i] = or_expf(A[i % heads] * sp);
+        Strength[i] = or_sigmoid(Beta[i]);
+    }
+}
+/* kernels/strata.cu:432-445 strata_gdn_batch: each (head, component)'s tokens in order. */
+void or_gdn_batch(float *State, const float *Q, const float *K, const float *V, const float *Decay, const float *Beta,
+                  float *Y, int dim, int keyHeads, int valueHeads, int tokens) {
+    int stride = valueHeads * dim;
+    for (int jh = 0; jh < dim * valueHeads; jh++) {
+        int h = jh / dim, kh = h % keyHeads;
+        for (int token = 0; token < tokens; ++token) {
+            int qbase = (token * keyHeads + kh) * dim, gh = token * valueHeads + h;
+            float prediction = 0.0f;
+            for (int i = 0; i < dim; ++i) {
+                int ix = i * stride + jh;
+                State[ix] *= Decay[gh];
+                prediction += State[ix] * K[qbase + i];
+            }
+            float delta = (V[token * stride + jh] - prediction) * Beta[gh], result = 0.0f;
+            for (int i = 0; i < dim; ++i) {
+                int ix = i * stride + jh;
+                State[ix] += K[qbase + i] * delta;
+                result += State[ix] * Q[qbase + i];
+            }
+            Y[token * stride + jh] = result;
+        }
+    }
+}
+/* kernels/strata.cu:446-453 strata_rope_batch: token t at table row t. */
+void or_rope_batch(const float *X, const float *Cos, const float *Sin, float *Y, int dim, int heads, int rotary,
+                   int tokens) {
+    int half = rotary / 2;
+    for (int i = 0; i < dim * heads * tokens; i++) {
+        int d = i % dim;
+        if (d >= rotary) { Y[i] = X[i]; continue; }
+        int pair = d % half, base = i - d, angle = (i / (dim * heads)) * half + pair;
+        float a = X[base + pair], b = X[base + pair + half];
+        Y[i] = d < half ? a * Cos[angle] - b * Sin[angle] : b * Cos[angle] + a * Sin[angle];
+    }
+}
+/* kernels/strata.cu:454-457 strata_kv_append_batch */
+void or_kv_append_batch(const float *K, const float *V, float *Keys, float *Values, int width, int position,
+                        int tokens) {
+    for (int i = 0; i < width * tokens; i++) {
+        Keys[position * width + i] = K[i];
+        Values[position * width + i] = V[i];
+    }
+}
+/* kernels/strata.cu:458-460 strata_attention_gate_batch */
+void or_attention_gate_batch(const float *Attention, const float *FullQ, float *Y, int dim, int heads, int tokens) {
+    for (int i = 0; i < dim * heads * tokens; i++)
+        Y[i] = Attention[i] * or_sigmoid(FullQ[(i / dim) * dim * 2 + dim + i % dim]);
+}
+/* kernels/strata.cu:461-464 strata_ple_broadcast_batch */
+void or_ple_broadcast_batch(const float *Value, const float *Gate, float *Y, int width, int streams, int tokens) {
+    int hc = width * streams;
+    for (int i = 0; i < hc * tokens; i++) Y[i] = Value[(i / hc) * width + i % width] * Gate[i / width];
+}
+/* kernels/strata.cu:512-534 strata_attention_batch: token t of the prompt
+ * attends to cells 0 .. position + t (all rows already appended). */
+void or_attention_batch(const float *Q, const float *Keys, const float *Values, float *Y, int dim, int heads,
+                        int kvHeads, int position, float scale, int tokens) {
+    static float scores[2048];
+    for (int token = 0; token < tokens; token++)
+        for (int h = 0; h < heads; h++) {
+            float part[LANES];
+            int count = position + token + 1, kh = h / (heads / kvHeads);
+            for (int l = 0; l < LANES; l++) {
+                float mx = NEG_BIG;
+                for (int t = l; t < count; t += LANES) {
+                    int base = (t * kvHeads + kh) * dim;
+                    float score = 0.0f;
+                    for (int j = 0; j < dim; ++j) score += Q[(token * heads + h) * dim + j] * Keys[base + j];
+                    score *= scale;
+                    scores[t] = score;
+                    mx = fmaxf(mx, score);
+                }
+                part[l] = mx;
+            }
+            float mx = tree_max64(part);
+            for (int l = 0; l < LANES; l++) {
+                float sum = 0.0f;
+                for (int t = l; t < count; t += LANES) {
+                    float p = or_expf(scores[t] - mx);
+                    scores[t] = p;
+                    sum += p;
+                }
+                part[l] = sum;
+            }
+            float total = tree_sum64(part);
+            for (int d = 0; d < dim; d++) {
+                float value = 0.0f;
+                for (int t = 0; t < count; ++t) value += scores[t] * Values[(t * kvHeads + kh) * dim + d];
+                Y[(token * heads + h) * dim + d] = value / total;
+            }
+        }
+}
+
 /* ------------------------------------------------------------ self checks --- */
 /* Counts, over float bit patterns u = start, start+step, ... < end, the inputs
  * where fn (0 logf, 1 sinf, 2 cosf) differs from this platform's libm (out[0])
