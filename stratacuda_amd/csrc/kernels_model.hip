@@ -315,6 +315,147 @@ __global__ void k_rope(const float *X, const float *Cos, const float *Sin, float
     Y[i] = d < half ? a * Cos[pair] - b * Sin[pair] : b * Cos[pair] + a * Sin[pair];
 }
 
+// ------------------------------------------------ prompt (batch) kernels
+// kernels/strata.cu:399-402
+__global__ void k_embed_batch(const float *Rows, float *Residual, int width, int hc, int n) {
+    int i = item();
+    if (i < n) Residual[i] = Rows[(i / hc) * width + i % width];
+}
+// kernels/strata.cu:403-408
+__global__ void k_hc_mix_batch(const float *Norm, const float *Gate, float *Mixed, int width, int streams, int n) {
+    int i = item();
+    if (i >= n) return;
+    int token = i / width, d = i % width;
+    float v = 0.0f;
+    for (int c = 0; c < streams; ++c) {
+        int p = (token * streams + c) * width + d;
+        v = v + Norm[p] * sm::sigmoid(Gate[p]);
+    }
+    Mixed[i] = v / (float)streams;
+}
+// kernels/strata.cu:409-412
+__global__ void k_hc_write_batch(float *Residual, const float *Output, const float *Inject, int width, int streams,
+                                 int n) {
+    int i = item();
+    if (i >= n) return;
+    int hc = width * streams;
+    Residual[i] = Residual[i] +
+                  Output[(i / hc) * width + i % width] * (2.0f * sm::sigmoid(Inject[i / width] / (float)streams));
+}
+// kernels/strata.cu:413-424: one channel per lane, its tokens in order.
+__global__ void k_conv_batch(float *History, const float *X, const float *W, float *Y, int channels, int taps,
+                             int dilation, int activation, int tokens, int n) {
+    int c = item();
+    if (c >= n) return;
+    int span = (taps - 1) * dilation;
+    float *h = History + (int64_t)c * span;
+    for (int token = 0; token < tokens; ++token) {
+        float sum = 0.0f;
+        for (int t = 0; t < taps - 1; ++t) sum = sum + h[t * dilation] * W[c * taps + t];
+        const float x = X[token * channels + c];
+        sum = sum + x * W[c * taps + taps - 1];
+        Y[token * channels + c] = activation == 1 ? sm::silu(sum) : sum;
+        for (int t = 0; t < span - 1; ++t) h[t] = h[t + 1];
+        if (span > 0) h[span - 1] = x;
+    }
+}
+// kernels/strata.cu:425-431
+__global__ void k_gdn_gates_batch(const float *Alpha, const float *Beta, const float *A, const float *Dt,
+                                  float *Decay, float *Strength, int heads, int n) {
+    int i = item();
+    if (i >= n) return;
+    float x = Alpha[i] + Dt[i % heads];
+    float sp = x > 20.0f ? x : sm::logf_or(1.0f + sm::expf_or(x));
+    Decay[i] = sm::expf_or(A[i % heads] * sp);
+    Strength[i] = sm::sigmoid(Beta[i]);
+}
+// kernels/strata.cu:432-445: one (value head, component) per lane, its tokens in order.
+__global__ void k_gdn_batch(float *State, const float *Q, const float *K, const float *V, const float *Decay,
+                            const float *Beta, float *Y, int dim, int keyHeads, int valueHeads, int tokens, int n) {
+    int jh = item();
+    if (jh >= n) return;
+    int h = jh / dim, kh = h % keyHeads, stride = valueHeads * dim;
+    for (int token = 0; token < tokens; ++token) {
+        const int qbase = (token * keyHeads + kh) * dim, gh = token * valueHeads + h;
+        const float decay = Decay[gh];
+        float prediction = 0.0f;
+        for (int i = 0; i < dim; ++i) {
+            int ix = i * stride + jh;
+            float s = State[ix] * decay;
+            State[ix] = s;
+            prediction = prediction + s * K[qbase + i];
+        }
+        float delta = (V[token * stride + jh] - prediction) * Beta[gh], result = 0.0f;
+        for (int i = 0; i < dim; ++i) {
+            int ix = i * stride + jh;
+            float s = State[ix] + K[qbase + i] * delta;
+            State[ix] = s;
+            result = result + s * Q[qbase + i];
+        }
+        Y[token * stride + jh] = result;
+    }
+}
+// kernels/strata.cu:446-453: token t rotated by table row t.
+__global__ void k_rope_batch(const float *X, const float *Cos, const float *Sin, float *Y, int dim, int heads,
+                             int rotary, int n) {
+    int i = item();
+    if (i >= n) return;
+    int d = i % dim;
+    if (d >= rotary) {
+        Y[i] = X[i];
+        return;
+    }
+    int half = rotary / 2, pair = d % half, base = i - d, angle = (i / (dim * heads)) * half + pair;
+    float a = X[base + pair], b = X[base + pair + half];
+    Y[i] = d < half ? a * Cos[angle] - b * Sin[angle] : b * Cos[angle] + a * Sin[angle];
+}
+// kernels/strata.cu:454-457
+__global__ void k_kv_append_batch(const float *K, const float *V, float *Keys, float *Values, int width, int position,
+                                  int n) {
+    int i = item();
+    if (i >= n) return;
+    Keys[position * width + i] = K[i];
+    Values[position * width + i] = V[i];
+}
+// kernels/strata.cu:461-464
+__global__ void k_ple_broadcast_batch(const float *Value, const float *Gate, float *Y, int width, int hc, int n) {
+    int i = item();
+    if (i < n) Y[i] = Value[(i / hc) * width + i % width] * Gate[i / width];
+}
+// kernels/strata.cu:512-534: one 64-lane block per (head, 64-component tile,
+// prompt token t), attending to cells 0 .. position + t.
+__global__ __launch_bounds__(64) void k_attention_batch(const float *Q, const float *Keys, const float *Values,
+                                                        float *Y, int dim, int heads, int kvHeads, int position,
+                                                        float scale) {
+    __shared__ float scores[2048];
+    const int token = blockIdx.z, count = position + token + 1, lane = threadIdx.x, h = blockIdx.x;
+    const int d = blockIdx.y * 64 + lane, kh = h / (heads / kvHeads);
+    const float *q = Q + (int64_t)(token * heads + h) * dim;
+    float mx = kNegBig;
+    for (int t = lane; t < count; t += 64) {
+        const float *k = Keys + (int64_t)(t * kvHeads + kh) * dim;
+        float score = 0.0f;
+        for (int j = 0; j < dim; ++j) score = score + q[j] * k[j];
+        score = score * scale;
+        scores[t] = score;
+        mx = fmaxf(mx, score);
+    }
+    for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_down(mx, s, 64));
+    mx = __shfl(mx, 0, 64);
+    float sum = 0.0f;
+    for (int t = lane; t < count; t += 64) {
+        float p = sm::expf_or(scores[t] - mx);
+        scores[t] = p;
+        sum = sum + p;
+    }
+    float total = __shfl(sm::tree_sum64(sum), 0, 64);
+    __syncthreads();
+    if (d >= dim) return;
+    float value = 0.0f;
+    for (int t = 0; t < count; ++t) value = value + scores[t] * Values[(int64_t)(t * kvHeads + kh) * dim + d];
+    Y[(int64_t)(token * heads + h) * dim + d] = value / total;
+}
+
 // ------------------------------------------------------------- launchers
 int bad(sm_ctx *ctx, const std::string &m) { return fail(ctx, SM_E_ARG, m); }
 unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -605,6 +746,170 @@ int L_rope(sm_ctx *ctx, const uint32_t *G, Args a) {
     return launched(ctx);
 }
 
+// Largest index + 1 of Rows[(i / hc) * width + i % width] over i < n.
+int64_t row_span(int64_t n, int width, int64_t hc) {
+    const int64_t tl = (n - 1) / hc;
+    return tl * width + std::min<int64_t>(width, n - tl * hc);
+}
+
+int L_embed_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(2), streams = a.i32(3), tokens = a.i32(4);
+    if (width < 1 || streams < 1 || tokens < 1) return bad(ctx, "strata_embed_batch: width, streams, tokens >= 1");
+    const int64_t hc = (int64_t)width * streams, n = covered(G, hc * tokens);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)row_span(n, width, hc) * 4, "Rows")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "Residual")) return rc;
+    k_embed_batch<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), Fw(a, 1), width, (int)hc, (int)n);
+    return launched(ctx);
+}
+
+int L_hc_mix_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4), tokens = a.i32(5);
+    if (width < 1 || streams < 1 || tokens < 1) return bad(ctx, "strata_hc_mix_batch: width, streams, tokens >= 1");
+    const int64_t n = covered(G, (int64_t)width * tokens), tl = (n - 1) / width;
+    const uint64_t span = (uint64_t)((tl * streams + streams - 1) * width + (n - tl * width)) * 4;
+    if (int rc = need(ctx, a.ptr(0), span, "Norm")) return rc;
+    if (int rc = need(ctx, a.ptr(1), span, "Gate")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Mixed")) return rc;
+    k_hc_mix_batch<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), width, streams, (int)n);
+    return launched(ctx);
+}
+
+int L_hc_write_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4), tokens = a.i32(5);
+    if (width < 1 || streams < 1 || tokens < 1) return bad(ctx, "strata_hc_write_batch: width, streams, tokens >= 1");
+    const int64_t hc = (int64_t)width * streams, n = covered(G, hc * tokens);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "Residual")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)row_span(n, width, hc) * 4, "Output")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)((n - 1) / width + 1) * 4, "Inject")) return rc;
+    k_hc_write_batch<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), width, streams, (int)n);
+    return launched(ctx);
+}
+
+int L_conv_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int channels = a.i32(4), taps = a.i32(5), dilation = a.i32(6), activation = a.i32(7), tokens = a.i32(8);
+    if (channels < 1 || taps < 1 || dilation < 1 || tokens < 1)
+        return bad(ctx, "strata_conv_batch: channels, taps, dilation and tokens must be >= 1");
+    const int64_t n = covered(G, channels), span = (int64_t)(taps - 1) * dilation;
+    const uint64_t xy = (uint64_t)((int64_t)(tokens - 1) * channels + n) * 4;
+    if (span > 0)
+        if (int rc = need(ctx, a.ptr(0), (uint64_t)(n * span) * 4, "History")) return rc;
+    if (int rc = need(ctx, a.ptr(1), xy, "X")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)(n * taps) * 4, "W")) return rc;
+    if (int rc = need(ctx, a.ptr(3), xy, "Y")) return rc;
+    k_conv_batch<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), Fw(a, 3), channels, taps, dilation,
+                                                        activation, tokens, (int)n);
+    return launched(ctx);
+}
+
+int L_gdn_gates_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int heads = a.i32(6), tokens = a.i32(7);
+    if (heads < 1 || tokens < 1) return bad(ctx, "strata_gdn_gates_batch: heads and tokens must be >= 1");
+    const int64_t n = covered(G, (int64_t)heads * tokens), per = std::min<int64_t>(n, heads);
+    const int idx[6] = {0, 1, 2, 3, 4, 5};
+    const char *names[6] = {"Alpha", "Beta", "A", "Dt", "Decay", "Strength"};
+    for (int i : idx)
+        if (int rc = need(ctx, a.ptr(i), (uint64_t)(i == 2 || i == 3 ? per : n) * 4, names[i])) return rc;
+    k_gdn_gates_batch<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), F(a, 3), Fw(a, 4), Fw(a, 5),
+                                                             heads, (int)n);
+    return launched(ctx);
+}
+
+int L_gdn_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(7), keyHeads = a.i32(8), valueHeads = a.i32(9), tokens = a.i32(10);
+    if (dim < 1 || keyHeads < 1 || valueHeads < 1 || tokens < 1)
+        return bad(ctx, "strata_gdn_batch: dim, keyHeads, valueHeads and tokens must be >= 1");
+    const int64_t stride = (int64_t)valueHeads * dim, n = covered(G, stride), heads = (n - 1) / dim + 1;
+    const int64_t khs = std::min<int64_t>(keyHeads, heads);
+    const uint64_t qk = (uint64_t)(((int64_t)(tokens - 1) * keyHeads + khs) * dim) * 4;
+    const uint64_t vy = (uint64_t)((int64_t)(tokens - 1) * stride + n) * 4;
+    const uint64_t gb = (uint64_t)((int64_t)(tokens - 1) * valueHeads + heads) * 4;
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)((int64_t)(dim - 1) * stride + n) * 4, "State")) return rc;
+    if (int rc = need(ctx, a.ptr(1), qk, "Q")) return rc;
+    if (int rc = need(ctx, a.ptr(2), qk, "K")) return rc;
+    if (int rc = need(ctx, a.ptr(3), vy, "V")) return rc;
+    if (int rc = need(ctx, a.ptr(4), gb, "Decay")) return rc;
+    if (int rc = need(ctx, a.ptr(5), gb, "Beta")) return rc;
+    if (int rc = need(ctx, a.ptr(6), vy, "Y")) return rc;
+    k_gdn_batch<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), F(a, 3), F(a, 4), F(a, 5), Fw(a, 6),
+                                                       dim, keyHeads, valueHeads, tokens, (int)n);
+    return launched(ctx);
+}
+
+int L_rope_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(4), heads = a.i32(5), rotary = a.i32(6), tokens = a.i32(7);
+    if (dim < 1 || heads < 1 || rotary < 1 || tokens < 1) return bad(ctx, "strata_rope_batch: dim, heads, rotary, tokens >= 1");
+    if (rotary % 2 || rotary > dim) return bad(ctx, "Rotary width must be even and <= head dimension");
+    const int64_t n = covered(G, (int64_t)dim * heads * tokens);
+    const uint64_t table = (uint64_t)(((n - 1) / ((int64_t)dim * heads) + 1) * (rotary / 2)) * 4;
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)((n - 1) / dim + 1) * dim * 4, "X")) return rc;
+    if (int rc = need(ctx, a.ptr(1), table, "Cos")) return rc;
+    if (int rc = need(ctx, a.ptr(2), table, "Sin")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)n * 4, "Y")) return rc;
+    k_rope_batch<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3), dim, heads, rotary, (int)n);
+    return launched(ctx);
+}
+
+int L_kv_append_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(4), position = a.i32(5), tokens = a.i32(6);
+    if (width < 1 || position < 0 || tokens < 1)
+        return bad(ctx, "strata_kv_append_batch: width >= 1, position >= 0, tokens >= 1");
+    const int64_t n = covered(G, (int64_t)width * tokens);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "K")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)n * 4, "V")) return rc;
+    const uint64_t end = (uint64_t)((int64_t)position * width + n) * 4;
+    if (int rc = need(ctx, a.ptr(2), end, "Keys")) return rc;
+    if (int rc = need(ctx, a.ptr(3), end, "Values")) return rc;
+    k_kv_append_batch<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), Fw(a, 3), width, position,
+                                                             (int)n);
+    return launched(ctx);
+}
+
+int L_attention_gate_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(3), heads = a.i32(4), tokens = a.i32(5);
+    if (dim < 1 || heads < 1 || tokens < 1) return bad(ctx, "strata_attention_gate_batch: dim, heads, tokens >= 1");
+    const int64_t n = covered(G, (int64_t)dim * heads * tokens), last = n - 1;
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)n * 4, "Attention")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)((last / dim) * dim * 2 + dim + last % dim + 1) * 4, "FullQ"))
+        return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Y")) return rc;
+    k_attention_gate<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), dim, (int)n);
+    return launched(ctx);
+}
+
+int L_ple_broadcast_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int width = a.i32(3), streams = a.i32(4), tokens = a.i32(5);
+    if (width < 1 || streams < 1 || tokens < 1) return bad(ctx, "strata_ple_broadcast_batch: width, streams, tokens >= 1");
+    const int64_t hc = (int64_t)width * streams, n = covered(G, hc * tokens);
+    if (int rc = need(ctx, a.ptr(0), (uint64_t)row_span(n, width, hc) * 4, "Value")) return rc;
+    if (int rc = need(ctx, a.ptr(1), (uint64_t)((n - 1) / width + 1) * 4, "Gate")) return rc;
+    if (int rc = need(ctx, a.ptr(2), (uint64_t)n * 4, "Y")) return rc;
+    k_ple_broadcast_batch<<<blocks256(n), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), Fw(a, 2), width, (int)hc, (int)n);
+    return launched(ctx);
+}
+
+// src/backend.js:44-49: the prompt's token count is Q's length over heads x dim.
+int L_attention_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
+    int dim = a.i32(4), heads = a.i32(5), kvHeads = a.i32(6), position = a.i32(7);
+    float scale = a.f32(8);
+    if (dim < 1 || heads < 1 || kvHeads < 1) return bad(ctx, "strata_attention_batch: dim, heads, kvHeads >= 1");
+    if (heads % kvHeads) return fail(ctx, SM_E_ARG, "Attention heads must be divisible by KV heads");
+    if (position < 0 || position > 2047) return bad(ctx, "attention position must be an integer in [0, 2047]");
+    const int64_t qlen = buf_len(ctx, a.ptr(0)), row = (int64_t)heads * dim * 4;
+    if (qlen < 0) return need(ctx, a.ptr(0), 0, "Q");
+    if (qlen % row || position + qlen / row > 2048) return fail(ctx, SM_E_ARG, "Batched attention exceeds 2048 cells");
+    const int tokens = (int)(qlen / row);
+    const int tu = (int)std::min<int64_t>(G[2], tokens), hu = (int)std::min<int64_t>(G[0], heads);
+    const int tiles = (int)std::min<int64_t>(G[1], (dim + 63) / 64);
+    if (tu < 1) return SM_OK;
+    const uint64_t kv = (uint64_t)(position + tu) * kvHeads * dim * 4;
+    if (int rc = need(ctx, a.ptr(1), kv, "Keys")) return rc;
+    if (int rc = need(ctx, a.ptr(2), kv, "Values")) return rc;
+    if (int rc = need(ctx, a.ptr(3), (uint64_t)((int64_t)(tu - 1) * heads + hu) * dim * 4, "Y")) return rc;
+    k_attention_batch<<<dim3(hu, tiles, tu), 64, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3), dim, heads,
+                                                                   kvHeads, position, scale);
+    return launched(ctx);
+}
+
 // Parameter lists in the reference's order (kernels/strata.cu).
 const Entry kModelEntries[] = {
     {"strata_embedding",
@@ -635,6 +940,27 @@ const Entry kModelEntries[] = {
     {"strata_ple_decode", "Packed:u32*,Values:f32*,count:i32", 3, L_ple_decode},
     {"strata_embed", "Row:f32*,Residual:f32*,width:i32,streams:i32", 4, L_embed},
     {"strata_rope", "X:f32*,Cos:f32*,Sin:f32*,Y:f32*,dim:i32,heads:i32,rotary:i32", 7, L_rope},
+    {"strata_embed_batch", "Rows:f32*,Residual:f32*,width:i32,streams:i32,tokens:i32", 5, L_embed_batch},
+    {"strata_hc_mix_batch", "Norm:f32*,Gate:f32*,Mixed:f32*,width:i32,streams:i32,tokens:i32", 6, L_hc_mix_batch},
+    {"strata_hc_write_batch", "Residual:f32*,Output:f32*,Inject:f32*,width:i32,streams:i32,tokens:i32", 6,
+     L_hc_write_batch},
+    {"strata_conv_batch",
+     "History:f32*,X:f32*,W:f32*,Y:f32*,channels:i32,taps:i32,dilation:i32,activation:i32,tokens:i32", 9,
+     L_conv_batch},
+    {"strata_gdn_gates_batch", "Alpha:f32*,Beta:f32*,A:f32*,Dt:f32*,Decay:f32*,Strength:f32*,heads:i32,tokens:i32", 8,
+     L_gdn_gates_batch},
+    {"strata_gdn_batch",
+     "State:f32*,Q:f32*,K:f32*,V:f32*,Decay:f32*,Beta:f32*,Y:f32*,dim:i32,keyHeads:i32,valueHeads:i32,tokens:i32", 11,
+     L_gdn_batch},
+    {"strata_rope_batch", "X:f32*,Cos:f32*,Sin:f32*,Y:f32*,dim:i32,heads:i32,rotary:i32,tokens:i32", 8, L_rope_batch},
+    {"strata_kv_append_batch", "K:f32*,V:f32*,Keys:f32*,Values:f32*,width:i32,position:i32,tokens:i32", 7,
+     L_kv_append_batch},
+    {"strata_attention_gate_batch", "Attention:f32*,FullQ:f32*,Y:f32*,dim:i32,heads:i32,tokens:i32", 6,
+     L_attention_gate_batch},
+    {"strata_ple_broadcast_batch", "Value:f32*,Gate:f32*,Y:f32*,width:i32,streams:i32,tokens:i32", 6,
+     L_ple_broadcast_batch},
+    {"strata_attention_batch",
+     "Q:f32*,Keys:f32*,Values:f32*,Y:f32*,dim:i32,heads:i32,kvHeads:i32,position:i32,scale:f32", 9, L_attention_batch},
 };
 
 }  // namespace

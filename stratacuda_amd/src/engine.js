@@ -15,6 +15,7 @@ import {performance} from 'perf_hooks';
 import {Ops, grid} from './ops.js';
 import {validateGeometry} from './model.js';
 import {ModelResidency} from './residency.js';
+import {prefillChunks} from './prefill.js';
 
 const shapeKey = shape => {
     const s = Array.from(shape);
@@ -167,15 +168,17 @@ export class StrataEngine {
     }
     // src/engine.js:125-132: one expert; f32 experts run as three projections
     // and the SiLU(gate)*up elementwise pass, Q2-packed ones from their blob.
-    async expert(prefix, x, shared) {
+    async expert(prefix, x, shared, tokens) {
+        tokens = tokens || 1;
         const o = this.ops, manifest = this.store.manifest;
         if (!shared && manifest && manifest.experts && manifest.experts.source_type === 'Q2_0') {
             const m = /^blk\.(\d+)\.expert\.(\d+)\.$/.exec(prefix);
-            return o.packedExpert(Number(m[1]), Number(m[2]), x, 1);
+            return o.packedExpert(Number(m[1]), Number(m[2]), x, tokens);
         }
         const name = role => shared ? prefix + 'ffn_' + role + '_shexp.weight' : prefix + role;
-        const gate = await o.mat(name('gate'), x), up = await o.mat(name('up'), x), activation = await o.elem(gate, up, 3);
-        return o.mat(name('down'), activation);
+        const gate = await o.mat(name('gate'), x, tokens), up = await o.mat(name('up'), x, tokens);
+        const activation = await o.elem(gate, up, 3);
+        return o.mat(name('down'), activation, tokens);
     }
     // src/engine.js:133-156: router, routing check, routed experts into their
     // slots, shared expert and gate, combine.
@@ -205,6 +208,25 @@ export class StrataEngine {
         return y;
     }
     residencyInfo() { return this.ops.residency.info(); }
+    // src/engine.js:158-165: the prompt in layer-major chunks (src/prefill.js).
+    async prefill(tokens, options) {
+        const o = options || {};
+        this.assertIdle('A session operation is already running');
+        if (this.failed) throw Error('Session failed; reset it before continuing');
+        tokens = Array.from(tokens);
+        if (!tokens.length) throw Error('Prompt is empty');
+        for (const t of tokens)
+            if (!Number.isSafeInteger(t) || t < 0 || t > this.g.vocab - 1)
+                throw new RangeError('token must be an integer in [0, ' + (this.g.vocab - 1) + ']');
+        if (this.position + tokens.length > this.g.context) throw Error('Context capacity reached');
+        const chunk = o.chunkSize === undefined ? 16 : o.chunkSize;
+        if (!Number.isSafeInteger(chunk) || chunk < 1 || chunk > 64)
+            throw new RangeError('prompt chunk size must be an integer in [1, 64]');
+        if (o.logits && o.predict === false) throw Error('Logits require prediction');
+        this.busy = true;
+        try { return await prefillChunks(this, tokens, o); } catch (error) { this.failed = true; throw error; }
+        finally { this.busy = false; }
+    }
     // src/engine.js:166-196.
     async step(token, options) {
         const opts = options || {}, logits = !!opts.logits, predict = opts.predict !== false;

@@ -88,4 +88,27 @@ test('seeded token trace for the oracle comparison', async () => {
     } finally { await e.dispose(); }
 });
 
+// tests/conformance.js:84-92: prompt chunks of 1, 2 and 5 at a nonzero start,
+// then the next decode step; logits bits go to prompt.json for the oracle.
+test('prompt chunks 1, 2, 5 after a decode step, then decode 8', async () => {
+    const e = await engine(), out = [];
+    try {
+        for (const chunkSize of [1, 2, 5]) {
+            await e.reset();
+            await e.step(2, {predict: false});
+            const prompt = await e.prefill([7, 4, 8, 7, 4], {chunkSize, logits: true});
+            const routes = e.stats.routes.map(r => [r.position, r.layer, r.ids]);
+            assert.strictEqual(prompt.position, 5);
+            assert.strictEqual(e.position, 6);
+            const next = await e.step(8, {logits: true});
+            out.push({chunkSize, token: prompt.token, logits: bits(prompt.logits), routes,
+                nextToken: next.token, next: bits(next.logits)});
+        }
+        await assert.rejects(e.prefill([]), /Prompt is empty/);
+        await assert.rejects(e.prefill([1, 2], {chunkSize: 0}), RangeError);
+        await assert.rejects(e.prefill([1, 40]), RangeError);
+        fs.writeFileSync(path.join(dir, 'prompt.json'), JSON.stringify(out));
+    } finally { await e.dispose(); }
+});
+
 run().then(async () => { if (backend) await backend.dispose(); });

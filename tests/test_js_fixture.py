@@ -63,3 +63,22 @@ def test_js_fixture_decode_on_gpu(oracle, tmp_path):
     print("fixture decode: 16 steps, max |logit - oracle| = %.3g, bit-exact: %s" % (worst, exact))
     assert worst <= 1e-4
     assert exact
+    prompt = json.load(open(os.path.join(str(tmp_path), "prompt.json")))
+    assert [p["chunkSize"] for p in prompt] == [1, 2, 5]
+    for p in prompt:
+        e = fx.OracleEngine(fx.create_fixture(1234))
+        e.step(2, predict=False)
+        tok, logits = fx.prefill(e, [7, 4, 8, 7, 4], chunk_size=p["chunkSize"])
+        assert p["routes"] == [[r["position"], r["layer"], r["ids"]] for r in e.routes]
+        assert p["token"] == tok
+        same_bits(p["logits"], logits)
+        tok, logits = e.step(8)
+        assert p["nextToken"] == tok
+        same_bits(p["next"], logits)
+    print("fixture prompt chunks 1/2/5 + next decode: bit-exact with the oracle")
+
+
+def same_bits(got_bits, want):
+    got = np.array(got_bits, np.uint32)
+    assert np.array_equal(got, np.asarray(want, np.float32).view(np.uint32)), \
+        "max |diff| %g" % np.max(np.abs(got.view(np.float32).astype(np.float64) - want))
