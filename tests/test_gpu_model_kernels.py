@@ -262,7 +262,7 @@ def test_bf16_project_quant_gemv_ple_decode_embed_rope(backend, oracle):
                                           "codebook": 0, "hasOffset": 1}, [rows, 1, 1])
         same(backend.read(out), oracle.quant_gemv(xv, cw, sc, of, cols, rows, bits, gs, -3, 0, 1))
     # IQ4_NL PLE rows: 2560 values (80 blocks of 18 bytes)
-    raw = rng.integers(0, 256, 80 * 18 + 2, dtype=np.uint8)
+    raw = rng.integers(0, 256, 80 * 18, dtype=np.uint8)
     for b in range(80):
         raw[b * 18:b * 18 + 2] = np.frombuffer(np.float16(rng.normal(0, 0.02)).tobytes(), np.uint8)
     packed = np.frombuffer(raw.tobytes(), np.uint32).copy()
