@@ -165,6 +165,85 @@ def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefi
     return out
 
 
+def dense_formats(be, np, capture, replay, release, cols=2560, rows=10240, reps=200):
+    """Dense-format projections at the real model's width, one token (GEMV):
+    strata_bf16_project and strata_quant_gemv (S4, S8; group 32, offsets),
+    each over enough distinct weight copies (> 256 MiB) that every launch
+    reads its weights from HBM. Algorithmic bytes: the weights (codes +
+    scales + offsets) + x + y."""
+    out = {}
+    rng = np.random.default_rng(7)
+    x = be.alloc(rng.normal(0, 1, cols).astype(np.float32))
+    y = be.alloc(rows)
+    w = rng.normal(0, 0.05, rows * cols).astype(np.float32)
+    hi = (w.view(np.uint32) >> 16).astype(np.uint32)
+    del w
+    bf16 = (hi[0::2] | (hi[1::2] << 16)).astype(np.uint32)
+    del hi
+    gs = 32
+    cases = [("bf16_project", "strata_bf16_project", bf16, None)]
+    for bits in (4, 8):
+        codes = rng.integers(0, 2 ** 32, rows * cols * bits // 32, dtype=np.uint64).astype(np.uint32)
+        cases.append(("quant_gemv_s%d" % bits, "strata_quant_gemv", codes, bits))
+    for label, kernel, codes, bits in cases:
+        wbytes = codes.nbytes + (0 if bits is None else 2 * 4 * rows * cols // gs)
+        copies = max(2, -(-(320 << 20) // wbytes))
+        bufs = []
+        for _ in range(copies):
+            if bits is None:
+                bufs.append({"Codes": be.alloc(codes, "u32")})
+            else:
+                bufs.append({"Codes": be.alloc(codes, "u32"),
+                             "Scales": be.alloc(rng.normal(0, 0.02, rows * cols // gs).astype(np.float32)),
+                             "Offsets": be.alloc(rng.normal(0, 0.01, rows * cols // gs).astype(np.float32))})
+
+        def launch(i, b=bufs, kernel=kernel, bits=bits):
+            a = dict(b[i % len(b)], X=x, Y=y, cols=cols, rows=rows)
+            if bits is None:
+                a.update(tokens=1, outputStride=rows, outputOffset=0)
+                be.run(kernel, a, [rows, 1, 1])
+            else:
+                a.update(bits=bits, groupSize=gs, bias=-(1 << (bits - 1)), codebook=0, hasOffset=1)
+                be.run(kernel, a, [rows, 1, 1])
+
+        gid = capture(lambda: [launch(i) for i in range(reps)])
+        replay(gid)
+        be.sync()
+        be.event_record(8)
+        for _ in range(3):
+            replay(gid)
+        be.event_record(9)
+        be.sync()
+        us = be.event_elapsed_ms(8, 9) * 1e3 / (3 * reps)
+        nbytes = wbytes + cols * 4 + rows * 4
+        out[label] = {"cols": cols, "rows": rows, "avg_us": round(us, 3), "bytes_per_launch": nbytes,
+                      "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac_hbm": round(nbytes / (us * 1e-6) / PEAK_HBM, 4),
+                      "weight_copies": copies}
+        release(gid)
+        for b in bufs:
+            for v in b.values():
+                be.free(v)
+    be.free(x)
+    be.free(y)
+    return out
+
+
+def prompt_orchestration(timeout=300):
+    """The fixture prompt (24 tokens) through StrataEngine.prefill in chunks
+    and through step() token by token, in a Node.js child process."""
+    import shutil
+    import subprocess
+    node = shutil.which("node")
+    if node is None:
+        return {"skipped": "node not found"}
+    here = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([node, os.path.join(here, "stratacuda_amd", "src", "bench_prompt.js"), "24", "5"],
+                       cwd=here, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError("bench_prompt.js failed:\n" + r.stdout[-2000:])
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def read_traffic(kernel):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -360,6 +439,8 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the 48-layer stack runs")
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--no-pack", action="store_true", help="skip the pack-loading measurement")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense-format projection measurement")
+    ap.add_argument("--no-prompt", action="store_true", help="skip the fixture prompt measurement (Node.js)")
     ap.add_argument("--no-real", action="store_true",
                     help="skip the real model's geometry (hidden 2560, ff 640) runs")
     ap.add_argument("--no-cpu", action="store_true")
@@ -610,6 +691,10 @@ def main():
     if not args.no_real:
         real = real_model(be, wl, np, capture, replay, release)
 
+    dense = None
+    if not args.no_dense:
+        dense = dense_formats(be, np, capture, replay, release)
+
     # ---- pack loading: layer 0 written as a pack, then streamed back into HBM
     pack = None
     if not args.no_pack:
@@ -635,6 +720,10 @@ def main():
                     "GB_per_s": round(nbytes / dt / 1e9, 2), "arena_bit_exact": same}
         finally:
             shutil.rmtree(d, ignore_errors=True)
+
+    prompt = None
+    if not args.no_prompt:
+        prompt = prompt_orchestration()
 
     cpu = None
     if not args.no_cpu:
@@ -666,6 +755,8 @@ def main():
         "stack": stack,
         "real_model": real,
         "pack_load": pack,
+        "dense_formats": dense,
+        "prompt": prompt,
     }
     print(json.dumps(out))
     be.dispose()

@@ -50,6 +50,10 @@ __global__ void k_expert_scales(const uint32_t *Blob, float *Scales, int offset,
     if (i < count) Scales[i] = blob_half(Blob, (int64_t)offset + i);
 }
 
+// Positions per lane whose loads the projections issue together: a lane's
+// sum still takes them in the reference's order, so only latency changes.
+constexpr int PU = 8;
+
 // kernels/strata.cu:156-165 strata_project and :121-130 strata_gemv.
 __global__ void k_project(const float *X, const float *W, float *Y, int cols, int rows, int tokens, int outputStride,
                           int outputOffset, uint32_t gx, uint64_t total) {
@@ -59,7 +63,19 @@ __global__ void k_project(const float *X, const float *W, float *Y, int cols, in
     if (row >= rows || token >= tokens) return;
     const float *w = W + (int64_t)row * cols, *x = X + (int64_t)token * cols;
     float sum = 0.0f;
-    for (int i = lane; i < cols; i += 64) sum = sum + w[i] * x[i];
+    // The reference's lane-strided order; PU positions' loads go out first.
+    for (int i0 = lane; i0 < cols; i0 += PU * 64) {
+        float wv[PU], xv[PU];
+#pragma unroll
+        for (int u = 0; u < PU; u++) {
+            const int i = min(i0 + 64 * u, cols - 1);
+            wv[u] = w[i];
+            xv[u] = x[i];
+        }
+#pragma unroll
+        for (int u = 0; u < PU; u++)
+            if (i0 + 64 * u < cols) sum = sum + wv[u] * xv[u];
+    }
     sum = sm::tree_sum64(sum);
     if (lane == 0) Y[(int64_t)token * outputStride + outputOffset + row] = sum;
 }
@@ -73,10 +89,24 @@ __global__ void k_bf16_project(const float *X, const uint32_t *Codes, float *Y, 
     int row = (int)(g % gx), token = (int)(g / gx), lane = lane_id();
     if (row >= rows || token >= tokens) return;
     const float *x = X + (int64_t)token * cols;
+    const int64_t base = (int64_t)row * cols;
     float sum = 0.0f;
-    for (int i = lane; i < cols; i += 64) {
-        const int64_t ix = (int64_t)row * cols + i;
-        sum = sum + __uint_as_float(((Codes[ix / 2] >> ((ix % 2) * 16)) & 65535u) << 16) * x[i];
+    // The reference's lane-strided order; PU positions' loads (clamped to
+    // the row) go out before their products are added in order.
+    for (int i0 = lane; i0 < cols; i0 += PU * 64) {
+        uint32_t w[PU];
+        float xv[PU];
+#pragma unroll
+        for (int u = 0; u < PU; u++) {
+            const int i = min(i0 + 64 * u, cols - 1);
+            w[u] = Codes[(base + i) / 2];
+            xv[u] = x[i];
+        }
+#pragma unroll
+        for (int u = 0; u < PU; u++) {
+            const int64_t ix = base + i0 + 64 * u;
+            if (i0 + 64 * u < cols) sum = sum + __uint_as_float(((w[u] >> ((ix % 2) * 16)) & 65535u) << 16) * xv[u];
+        }
     }
     sum = sm::tree_sum64(sum);
     if (lane == 0) Y[(int64_t)token * outputStride + outputOffset + row] = sum;
@@ -163,15 +193,31 @@ __global__ void k_quant_project(const float *X, const uint32_t *Codes, const flo
     if (!logical_group(total, g)) return;
     int row = (int)(g % gx), token = (int)(g / gx), lane = lane_id();
     if (row >= rows || token >= tokens) return;
+    const float *x = X + (int64_t)token * cols;
     float sum = 0.0f;
-    for (int i = lane; i < cols; i += 64) {
-        int index = row * cols + i, bit = index * bits;
-        int code = (int)((Codes[bit / 32] >> (bit % 32)) & ((1u << bits) - 1u));
-        float value = codebook == 1 ? iq4(code) : (float)(code + bias);
-        int group = index / groupSize;
-        float weight = value * Scales[group];
-        if (hasOffset != 0) weight = weight + Offsets[group];
-        sum = sum + weight * X[(int64_t)token * cols + i];
+    // The reference's lane-strided order (index, bit and group in 31 bits,
+    // as the launcher checks); PU positions' loads go out first.
+    for (int i0 = lane; i0 < cols; i0 += PU * 64) {
+        uint32_t w[PU];
+        float sc[PU], of[PU], xv[PU];
+#pragma unroll
+        for (int u = 0; u < PU; u++) {
+            const int index = row * cols + min(i0 + 64 * u, cols - 1), bit = index * bits;
+            w[u] = Codes[bit / 32];
+            sc[u] = Scales[index / groupSize];
+            of[u] = hasOffset != 0 ? Offsets[index / groupSize] : 0.0f;
+            xv[u] = x[min(i0 + 64 * u, cols - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < PU; u++) {
+            if (i0 + 64 * u >= cols) break;
+            const int bit = (row * cols + i0 + 64 * u) * bits;
+            const int code = (int)((w[u] >> (bit % 32)) & ((1u << bits) - 1u));
+            const float value = codebook == 1 ? iq4(code) : (float)(code + bias);
+            float weight = value * sc[u];
+            if (hasOffset != 0) weight = weight + of[u];
+            sum = sum + weight * xv[u];
+        }
     }
     sum = sm::tree_sum64(sum);
     if (lane == 0) Y[(int64_t)token * outputStride + outputOffset + row] = sum;
