@@ -275,18 +275,21 @@ def cpu_baseline(oracle, wl, seconds):
 
 PROFILE_CMDS = {
     "trace": "rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/trace -o decode -- "
-             "python3 -u bench.py --no-cpu --eager --no-stack --steps 960",
+             "python3 -u bench.py --no-cpu --eager --no-stack --no-pack --no-prompt --steps 960",
     "fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_fetch -o decode -- "
-             "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --layers 8 --steps 16 --warmup 8",
+             "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --no-real --no-dense --no-pack --no-prompt "
+             "--layers 8 --steps 16 --warmup 8",
     "write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_write -o decode -- "
-             "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --layers 8 --steps 16 --warmup 8",
+             "python3 -u bench.py --no-cpu --eager --no-prefill --no-stack --no-real --no-dense --no-pack --no-prompt "
+             "--layers 8 --steps 16 --warmup 8",
     "cal_fetch": "rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/pmc_cal_fetch -o cal -- python3 -u bench.py --calibrate",
     "cal_write": "rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/pmc_cal_write -o cal -- python3 -u bench.py --calibrate",
 }
 for _case in ("512", "2048zipf"):
     PROFILE_CMDS["mfma_" + _case] = (
         "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_BUSY_CYCLES GRBM_GUI_ACTIVE "
-        "-f csv -d gpurun_out/pmc_mfma_%s -o prefill -- python3 -u bench.py --no-cpu --eager --no-stack --layers 2 "
+        "-f csv -d gpurun_out/pmc_mfma_%s -o prefill -- python3 -u bench.py --no-cpu --eager --no-stack --no-real "
+        "--no-dense --no-pack --no-prompt --layers 2 "
         "--steps 2 --warmup 2 --prefill-reps 4 --prefill-cases %s" % (_case, _case))
 # FLOPs per MFMA instruction: v_mfma_f32_32x32x16_f16 (64-row and register-B
 # kernels), v_mfma_f32_16x16x32_f16 (16-row kernels).
@@ -382,7 +385,8 @@ def summarize(out_dir):
     prof = os.path.join(ROOT, "profiles")
     os.makedirs(prof, exist_ok=True)
     stats = glob.glob(os.path.join(out_dir, "trace", "*kernel_stats.csv"))
-    lines = ["# Kernel durations: decode T=1 (48 rotated layers) and prefill T=512 / T=2048", "",
+    lines = ["# Kernel durations: decode T=1 (48 rotated layers), prefill T=512 / T=2048, the real model's "
+             "geometry (hidden 2560, ff 640) and the dense-format projections (2560 x 10240)", "",
              "Command (from the repository root):", "", "    " + PROFILE_CMDS["trace"], "",
              "| kernel | calls | avg us | min us | max us | share |", "|---|---|---|---|---|---|"]
     for r in _csv_rows(stats[0]):
