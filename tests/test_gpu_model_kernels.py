@@ -285,3 +285,40 @@ def test_bf16_project_quant_gemv_ple_decode_embed_rope(backend, oracle):
     with pytest.raises(sm.StrataError):  # count not a whole number of blocks
         backend.run("strata_ple_decode", {"Packed": backend.alloc(packed, "u32"), "Values": vals, "count": 100},
                     grid(100))
+
+
+@pytest.mark.parametrize("cols,rows,tokens", [(512, 9, 1), (4096, 5, 2), (300, 7, 2), (4608, 3, 1)])
+def test_bf16_project_shapes(backend, oracle, cols, rows, tokens):
+    """Row widths that are and are not whole 512-value (eight-load) batches,
+    one and two tokens: the reference's bits in every case."""
+    rng = np.random.default_rng(cols)
+    w = rng.normal(0, 0.05, rows * cols + 1).astype(np.float32)
+    hi = (w.view(np.uint32) >> 16).astype(np.uint32)
+    codes = (hi[0:-1:2] | (hi[1::2] << 16)).astype(np.uint32)
+    x = rng.normal(0, 1, tokens * cols).astype(np.float32)
+    y = backend.alloc(tokens * rows)
+    backend.run("strata_bf16_project", {"X": backend.alloc(x), "Codes": backend.alloc(codes, "u32"), "Y": y,
+                                        "cols": cols, "rows": rows, "tokens": tokens, "outputStride": rows,
+                                        "outputOffset": 0}, [rows, tokens, 1])
+    same(backend.read(y), oracle.bf16_project(x, codes, cols, rows, tokens, rows, 0,
+                                              Y=np.zeros(tokens * rows, np.float32)))
+
+
+@pytest.mark.parametrize("cols,bits,gs,has_offset", [(2560, 4, 32, 1), (2560, 8, 64, 0), (4096, 8, 16, 1),
+                                                      (96, 2, 32, 1), (4096, 2, 8, 0), (336, 4, 48, 1)])
+def test_quant_gemv_shapes(backend, oracle, cols, bits, gs, has_offset):
+    """S2 / S4 / S8 rows of 96 to 4096 values, groups of 8 to 64, with and
+    without offsets: the reference's bits in every case."""
+    rows = 11
+    rng = np.random.default_rng(cols * bits + gs)
+    cw = rng.integers(0, 2 ** 32, (cols * rows * bits + 31) // 32, dtype=np.uint64).astype(np.uint32)
+    sc = rng.normal(0, 0.03, cols * rows // gs).astype(np.float32)
+    of = rng.normal(0, 0.01, cols * rows // gs).astype(np.float32)
+    xv = rng.normal(0, 1, cols).astype(np.float32)
+    out = backend.alloc(rows)
+    bias = -(1 << (bits - 1))
+    backend.run("strata_quant_gemv", {"X": backend.alloc(xv), "Codes": backend.alloc(cw, "u32"),
+                                      "Scales": backend.alloc(sc), "Offsets": backend.alloc(of), "Y": out,
+                                      "cols": cols, "rows": rows, "bits": bits, "groupSize": gs, "bias": bias,
+                                      "codebook": 0, "hasOffset": has_offset}, [rows, 1, 1])
+    same(backend.read(out), oracle.quant_gemv(xv, cw, sc, of, cols, rows, bits, gs, bias, 0, has_offset))
