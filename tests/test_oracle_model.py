@@ -317,3 +317,28 @@ def test_partial_neox_rope_kat(oracle):
     s = np.sin(13 / 10000 ** (np.arange(2) / 2)).astype(np.float32)
     ref_compare(oracle.rope(x, c, s, 8, 3, 4), f64.rope(x.astype(np.float64), 8, 4, 13, 10000))
     assert np.array_equal(oracle.embed(x[:8], 8, 3), np.tile(x[:8], 3))
+
+
+def test_prompt_batches_equal_token_steps():
+    """Layer-major prompt batches (src/prefill.js) do each token's arithmetic
+    exactly as a decode step does, only grouped differently, so every chunk
+    size must give the step path's bits: the final logits and the state the
+    next step reads (KV cache, GDN state, conv and PLE histories)."""
+    from oracle import fixture as fx
+    rng = np.random.default_rng(11)
+    tokens = [int(t) for t in rng.integers(0, 40, 19)]
+    ref = fx.OracleEngine(fx.create_fixture(1234))
+    ref.step(3, predict=False)
+    for t in tokens[:-1]:
+        ref.step(t, predict=False)
+    want_tok, want = ref.step(tokens[-1])
+    after_tok, after = ref.step(9)
+    for chunk in (1, 3, 7, 19):
+        e = fx.OracleEngine(fx.create_fixture(1234))
+        e.step(3, predict=False)
+        tok, logits = fx.prefill(e, tokens, chunk_size=chunk)
+        assert tok == want_tok
+        assert np.array_equal(np.asarray(logits, np.float32).view(np.uint32), want.view(np.uint32)), chunk
+        tok, logits = e.step(9)
+        assert tok == after_tok
+        assert np.array_equal(np.asarray(logits, np.float32).view(np.uint32), after.view(np.uint32)), chunk
