@@ -88,8 +88,11 @@ int sm_sync(sm_ctx *ctx);
  * and the 17 that StrataEngine.step (src/engine.js:76-196) launches besides
  * them for the untrained fixture model (strata_embedding, strata_rope_*,
  * strata_hc_*, strata_conv, strata_gdn_*, strata_slice, strata_kv_append,
- * strata_attention[_gate], strata_ple_gate/_broadcast/_add, strata_argmax);
- * sm_kernel_name lists them. Cells / Mapping / Indices buffers are checked
+ * strata_attention[_gate], strata_ple_gate/_broadcast/_add, strata_argmax),
+ * the dense formats (strata_bf16_project, strata_quant_gemv, strata_ple_decode,
+ * strata_embed, strata_rope) and the 11 prompt-batch kernels that
+ * PromptBatch (src/prefill.js:5-97) launches (strata_*_batch): all 49 of
+ * kernels/strata.cu. sm_kernel_name lists them. Cells / Mapping / Indices buffers are checked
  * on the device before use (SM_E_BOUNDS), which synchronises the stream. */
 int sm_run(sm_ctx *ctx, const char *name, const uint32_t groups[3], const uint64_t *args, int nargs);
 int sm_kernel_count(void);
