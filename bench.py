@@ -228,6 +228,67 @@ def dense_formats(be, np, capture, replay, release, cols=2560, rows=10240, reps=
     return out
 
 
+def prompt_kernels(be, np, capture, replay, release, tokens=16, reps=50):
+    """The prompt-batch kernels at production shapes for one chunk of 16
+    tokens: GDN state update (128-wide keys, 16 key / 48 value heads), the
+    causal attention of the chunk at cells 2032-2047 (24 heads of 256, 2 KV
+    heads) and the 4-tap convolution over the GDN projection's 10240 channels.
+    Algorithmic bytes: state or cache read (and state written) once, plus
+    the chunk's inputs and outputs. Each launch reuses the same few MB, so
+    they are served from the 256 MiB Infinity Cache; frac_hbm only scales
+    the rate against the HBM peak."""
+    out = {}
+    rng = np.random.default_rng(5)
+    T = tokens
+    dim, kh, vh = 128, 16, 48
+    state = be.alloc(rng.normal(0, 0.1, dim * vh * dim).astype(np.float32))
+    q = be.alloc((rng.normal(0, 1, T * kh * dim) / np.sqrt(dim)).astype(np.float32))
+    k = be.alloc((rng.normal(0, 1, T * kh * dim) / np.sqrt(dim)).astype(np.float32))
+    v = be.alloc(rng.normal(0, 1, T * vh * dim).astype(np.float32))
+    dec = be.alloc(np.full(T * vh, 0.97, np.float32))
+    beta = be.alloc(np.full(T * vh, 0.5, np.float32))
+    y = be.alloc(T * vh * dim)
+    gdn = lambda: be.run("strata_gdn_batch", {"State": state, "Q": q, "K": k, "V": v, "Decay": dec, "Beta": beta,
+                                              "Y": y, "dim": dim, "keyHeads": kh, "valueHeads": vh, "tokens": T},
+                         [(vh * dim + 63) // 64, 1, 1])
+    gdn_bytes = 2 * dim * vh * dim * 4 + T * (2 * kh * dim + 2 * vh * dim + 2 * vh) * 4
+    ad, heads, kvh, pos = 256, 24, 2, 2048 - T
+    keys = be.alloc(rng.normal(0, 1, 2048 * kvh * ad).astype(np.float32))
+    values = be.alloc(rng.normal(0, 1, 2048 * kvh * ad).astype(np.float32))
+    aq = be.alloc(rng.normal(0, 1, T * heads * ad).astype(np.float32))
+    ay = be.alloc(T * heads * ad)
+    att = lambda: be.run("strata_attention_batch", {"Q": aq, "Keys": keys, "Values": values, "Y": ay, "dim": ad,
+                                                    "heads": heads, "kvHeads": kvh, "position": pos,
+                                                    "scale": 1 / 16.0}, [heads, ad // 64, T])
+    att_bytes = 2 * 2048 * kvh * ad * 4 + 2 * T * heads * ad * 4
+    ch = 2 * kh * dim + vh * dim
+    hist = be.alloc(ch * 3)
+    cx = be.alloc(rng.normal(0, 1, T * ch).astype(np.float32))
+    cw = be.alloc(rng.normal(0, 0.5, ch * 4).astype(np.float32))
+    cy = be.alloc(T * ch)
+    conv = lambda: be.run("strata_conv_batch", {"History": hist, "X": cx, "W": cw, "Y": cy, "channels": ch, "taps": 4,
+                                                "dilation": 1, "activation": 1, "tokens": T}, [(ch + 63) // 64, 1, 1])
+    conv_bytes = 2 * ch * 3 * 4 + 2 * T * ch * 4 + ch * 4 * 4
+    for label, fn, nbytes in (("gdn_batch", gdn, gdn_bytes), ("attention_batch", att, att_bytes),
+                              ("conv_batch", conv, conv_bytes)):
+        gid = capture(lambda: [fn() for _ in range(reps)])
+        replay(gid)
+        be.sync()
+        be.event_record(8)
+        for _ in range(3):
+            replay(gid)
+        be.event_record(9)
+        be.sync()
+        us = be.event_elapsed_ms(8, 9) * 1e3 / (3 * reps)
+        out[label] = {"tokens": T, "avg_us": round(us, 3), "bytes_per_launch": nbytes,
+                      "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                      "frac_hbm": round(nbytes / (us * 1e-6) / PEAK_HBM, 4)}
+        release(gid)
+    for b in (state, q, k, v, dec, beta, y, keys, values, aq, ay, hist, cx, cw, cy):
+        be.free(b)
+    return out
+
+
 def prompt_orchestration(timeout=300):
     """The fixture prompt (24 tokens) through StrataEngine.prefill in chunks
     and through step() token by token, in a Node.js child process."""
@@ -728,6 +789,7 @@ def main():
     prompt = None
     if not args.no_prompt:
         prompt = prompt_orchestration()
+        prompt["kernels"] = prompt_kernels(be, np, capture, replay, release)
 
     cpu = None
     if not args.no_cpu:

@@ -422,37 +422,109 @@ __global__ void k_ple_broadcast_batch(const float *Value, const float *Gate, flo
     int i = item();
     if (i < n) Y[i] = Value[(i / hc) * width + i % width] * Gate[i / width];
 }
-// kernels/strata.cu:512-534: one 64-lane block per (head, 64-component tile,
-// prompt token t), attending to cells 0 .. position + t.
-__global__ __launch_bounds__(64) void k_attention_batch(const float *Q, const float *Keys, const float *Values,
-                                                        float *Y, int dim, int heads, int kvHeads, int position,
-                                                        float scale) {
-    __shared__ float scores[2048];
-    const int token = blockIdx.z, count = position + token + 1, lane = threadIdx.x, h = blockIdx.x;
-    const int d = blockIdx.y * 64 + lane, kh = h / (heads / kvHeads);
+// The two longest prompt kernels with their memory round trips taken out and
+// the reference's arithmetic unchanged:
+//
+// k_gdn_batch_reg: k_gdn_batch with the thread's state column (dim <= 128
+// values) held in registers across the chunk's tokens instead of reread and
+// rewritten in memory twice per token; the products and sums are the same
+// operations in the same order, and the column is stored once at the end.
+constexpr int GDN_REG_MAX_DIM = 128;
+__global__ void __launch_bounds__(256) k_gdn_batch_reg(float *__restrict__ State, const float *__restrict__ Q,
+                                                       const float *__restrict__ K, const float *__restrict__ V,
+                                                       const float *__restrict__ Decay, const float *__restrict__ Beta,
+                                                       float *__restrict__ Y, int dim, int keyHeads, int valueHeads,
+                                                       int tokens, int n) {
+    int jh = item();
+    if (jh >= n) return;
+    const int h = jh / dim, kh = h % keyHeads, stride = valueHeads * dim;
+    float st[GDN_REG_MAX_DIM];
+#pragma unroll
+    for (int i = 0; i < GDN_REG_MAX_DIM; ++i)
+        if (i < dim) st[i] = State[i * stride + jh];
+    for (int token = 0; token < tokens; ++token) {
+        const int qbase = (token * keyHeads + kh) * dim, gh = token * valueHeads + h;
+        const float decay = Decay[gh];
+        float prediction = 0.0f;
+#pragma unroll
+        for (int i = 0; i < GDN_REG_MAX_DIM; ++i)
+            if (i < dim) {
+                st[i] = st[i] * decay;
+                prediction = prediction + st[i] * K[qbase + i];
+            }
+        const float delta = (V[token * stride + jh] - prediction) * Beta[gh];
+        float result = 0.0f;
+#pragma unroll
+        for (int i = 0; i < GDN_REG_MAX_DIM; ++i)
+            if (i < dim) {
+                st[i] = st[i] + K[qbase + i] * delta;
+                result = result + st[i] * Q[qbase + i];
+            }
+        Y[token * stride + jh] = result;
+    }
+#pragma unroll
+    for (int i = 0; i < GDN_REG_MAX_DIM; ++i)
+        if (i < dim) State[i * stride + jh] = st[i];
+}
+
+// k_attention_batch4 (kernels/strata.cu:512-534: cells 0 .. position + t for
+// prompt token t): one 256-thread block per (head, token) and four
+// 64-component tiles. The reference's 64-lane blocks of one (head, token)
+// all compute the same scores; here the four waves compute each score once
+// (cell t by wave (t / 64) % 4, same sequential dot over the head
+// dimension, loads issued eight at a time), then every wave forms the
+// maximum, the exponentials and their sum in the reference's lane order
+// (lane l: cells l, l + 64, ...; the same trees) and each wave runs the
+// weighted sum of its own tile, sequential over the cells.
+__global__ __launch_bounds__(256) void k_attention_batch4(const float *__restrict__ Q, const float *__restrict__ Keys,
+                                                          const float *__restrict__ Values, float *__restrict__ Y,
+                                                          int dim, int heads, int kvHeads, int position, float scale,
+                                                          int tiles) {
+    __shared__ float s_score[2048], s_prob[2048];
+    const int token = blockIdx.z, count = position + token + 1, h = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, kh = h / (heads / kvHeads);
     const float *q = Q + (int64_t)(token * heads + h) * dim;
-    float mx = kNegBig;
-    for (int t = lane; t < count; t += 64) {
+    for (int t = threadIdx.x; t < count; t += 256) {
         const float *k = Keys + (int64_t)(t * kvHeads + kh) * dim;
         float score = 0.0f;
-        for (int j = 0; j < dim; ++j) score = score + q[j] * k[j];
-        score = score * scale;
-        scores[t] = score;
-        mx = fmaxf(mx, score);
+        for (int j0 = 0; j0 < dim; j0 += 8) {
+            float kv[8], qv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = min(j0 + u, dim - 1);
+                kv[u] = k[j];
+                qv[u] = q[j];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (j0 + u < dim) score = score + qv[u] * kv[u];
+        }
+        s_score[t] = score * scale;
     }
+    __syncthreads();
+    float mx = kNegBig;
+    for (int t = lane; t < count; t += 64) mx = fmaxf(mx, s_score[t]);
     for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_down(mx, s, 64));
     mx = __shfl(mx, 0, 64);
     float sum = 0.0f;
     for (int t = lane; t < count; t += 64) {
-        float p = sm::expf_or(scores[t] - mx);
-        scores[t] = p;
+        const float p = sm::expf_or(s_score[t] - mx);
+        if (w == 0) s_prob[t] = p;
         sum = sum + p;
     }
-    float total = __shfl(sm::tree_sum64(sum), 0, 64);
+    const float total = __shfl(sm::tree_sum64(sum), 0, 64);
     __syncthreads();
-    if (d >= dim) return;
+    const int tile = blockIdx.y * 4 + w, d = tile * 64 + lane;
+    if (tile >= tiles || d >= dim) return;
     float value = 0.0f;
-    for (int t = 0; t < count; ++t) value = value + scores[t] * Values[(int64_t)(t * kvHeads + kh) * dim + d];
+    for (int t0 = 0; t0 < count; t0 += 8) {
+        float vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) vv[u] = Values[(int64_t)(min(t0 + u, count - 1) * kvHeads + kh) * dim + d];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (t0 + u < count) value = value + s_prob[t0 + u] * vv[u];
+    }
     Y[(int64_t)(token * heads + h) * dim + d] = value / total;
 }
 
@@ -830,8 +902,12 @@ int L_gdn_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
     if (int rc = need(ctx, a.ptr(4), gb, "Decay")) return rc;
     if (int rc = need(ctx, a.ptr(5), gb, "Beta")) return rc;
     if (int rc = need(ctx, a.ptr(6), vy, "Y")) return rc;
-    k_gdn_batch<<<blocks256(n), 256, 0, ctx->stream>>>(Fw(a, 0), F(a, 1), F(a, 2), F(a, 3), F(a, 4), F(a, 5), Fw(a, 6),
-                                                       dim, keyHeads, valueHeads, tokens, (int)n);
+    // The register-resident variant needs a column of at most 128 values and
+    // a State that no other argument aliases (the same handle twice).
+    bool distinct = true;
+    for (int i = 1; i < 7; i++) distinct = distinct && a.ptr(i) != a.ptr(0);
+    (dim <= GDN_REG_MAX_DIM && distinct ? k_gdn_batch_reg : k_gdn_batch)<<<blocks256(n), 256, 0, ctx->stream>>>(
+        Fw(a, 0), F(a, 1), F(a, 2), F(a, 3), F(a, 4), F(a, 5), Fw(a, 6), dim, keyHeads, valueHeads, tokens, (int)n);
     return launched(ctx);
 }
 
@@ -905,8 +981,9 @@ int L_attention_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
     if (int rc = need(ctx, a.ptr(1), kv, "Keys")) return rc;
     if (int rc = need(ctx, a.ptr(2), kv, "Values")) return rc;
     if (int rc = need(ctx, a.ptr(3), (uint64_t)((int64_t)(tu - 1) * heads + hu) * dim * 4, "Y")) return rc;
-    k_attention_batch<<<dim3(hu, tiles, tu), 64, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3), dim, heads,
-                                                                   kvHeads, position, scale);
+    k_attention_batch4<<<dim3(hu, (tiles + 3) / 4, tu), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3),
+                                                                                 dim, heads, kvHeads, position, scale,
+                                                                                 tiles);
     return launched(ctx);
 }
 
