@@ -66,6 +66,9 @@ const char *sm_last_error(sm_ctx *ctx);
 int sm_info(sm_ctx *ctx, char *buf, size_t cap);
 
 /* ---------------------------------------------------------------- buffers */
+/* zero != 0 clears the new buffer; refused (SM_E_ARG) while a graph is being
+ * captured. sm_zero while capturing records a fill kernel, not a memset, and
+ * takes whole 32-bit words only (offset and bytes multiples of 4). */
 int sm_alloc(sm_ctx *ctx, uint64_t bytes, int zero, uint64_t *handle);
 int sm_free(sm_ctx *ctx, uint64_t handle);
 int sm_size(sm_ctx *ctx, uint64_t handle, uint64_t *bytes);

@@ -65,6 +65,8 @@ def lib():
             "or_dispatch": (_i, [_i32p, _i, _i, _i, _i32p, _i32p, _i32p, _i32p]),
             "or_moe_layer": (_i, [_f32p, _i, _f32p, _vp, _u8p, _i64, _u8p, _f32p, _i, _i, _i, _i, _f32p,
                                   _i32p, _f32p, _vp]),
+            "or_set_threads": (None, [_i]),
+            "or_max_threads": (_i, []),
             "or_moe_block": (_i, [_f32p, _f32p, _i, _f32p, _f32p, _u8p, _i64, _u8p, _f32p, _i, _i, _i,
                                   _i, _i32p, _f32p]),
             "or_rand": (_u64, [_u64, _u64, _u64]),
@@ -245,6 +247,15 @@ def dispatch(ids, tokens, top_k, experts):
     if rc:
         raise ValueError("dispatch failed (%d)" % rc)
     return offsets, rows, parts, where
+
+
+def set_threads(n):
+    """OpenMP threads for the oracle's parallel loops."""
+    lib().or_set_threads(int(n))
+
+
+def max_threads():
+    return int(lib().or_max_threads())
 
 
 def moe_layer(X, tokens, Wr, arena, blob_stride, shared_blob, Wsg, width, ff, experts, top_k, bias=None,

@@ -30,11 +30,18 @@
 #include <stdint.h>
 #include <string.h>
 #include <stdlib.h>
+#include <omp.h>
 
 #define LANES 64
 
 /* ---------------------------------------------------------------- fp16 --- */
 /* kernels/strata.cu:13-18 strata_half_bits */
+/* Thread count of the OpenMP loops below (the CPU baseline times the oracle
+ * at the reference pool's default of 4 threads and its limit of 8,
+ * vendor/webcuda/src/wasm/thread-pool.hpp:49-50). */
+void or_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int or_max_threads(void) { return omp_get_max_threads(); }
+
 float or_half_bits(uint32_t h) {
     uint32_t sign = (h & 32768u) << 16, exponent = (h >> 10) & 31u, fraction = h & 1023u, bits;
     float out;

@@ -167,6 +167,8 @@ int sm_info(sm_ctx *ctx, char *buf, size_t cap) {
 int sm_alloc(sm_ctx *ctx, uint64_t bytes, int zero, uint64_t *handle) {
     if (!ctx || !handle) return SM_E_ARG;
     if (bytes == 0) return fail(ctx, SM_E_ARG, "allocation must be at least 1 byte");
+    // A zero fill would be a memset node in a captured graph.
+    if (zero && ctx->capturing) return fail(ctx, SM_E_ARG, "a zero-filled allocation is not allowed while capturing a graph");
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, bytes);
     if (e != hipSuccess) return fail(ctx, SM_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
@@ -238,7 +240,15 @@ int sm_copy(sm_ctx *ctx, uint64_t src, uint64_t src_offset, uint64_t dst, uint64
 int sm_zero(sm_ctx *ctx, uint64_t dst, uint64_t offset, uint64_t bytes) {
     if (!ctx) return SM_E_ARG;
     if (int rc = need(ctx, dst, offset + bytes, "zero")) return rc;
-    if (bytes) HIP_TRY(ctx, hipMemsetAsync((char *)dst + offset, 0, bytes, ctx->stream));
+    if (!bytes) return SM_OK;
+    if (ctx->capturing) {
+        // No memset node in a captured graph: a fill kernel instead, which
+        // clears whole 32-bit words only.
+        if (offset % 4 || bytes % 4)
+            return fail(ctx, SM_E_ARG, "while capturing a graph, zero takes whole 32-bit words");
+        return zero_words(ctx, (char *)dst + offset, bytes / 4);
+    }
+    HIP_TRY(ctx, hipMemsetAsync((char *)dst + offset, 0, bytes, ctx->stream));
     return SM_OK;
 }
 

@@ -69,3 +69,30 @@ def test_graph_replay_matches_eager(backend, layers, tokens, block):
             assert np.array_equal(bits(b.read(Y)), bits(ey)), "replay %d" % rep
     finally:
         b.graph_free(g)
+
+
+def test_capture_refuses_memsets_and_zero_fills_with_a_kernel(backend):
+    """While a graph is being captured, a zero-filled allocation is refused
+    and sm_zero records a fill kernel (no memset node): the replayed graph
+    clears the words each time, including after eager writes between
+    replays; a range that is not whole 32-bit words is refused."""
+    import stratacuda_amd as sm
+    b = backend
+    buf = b.alloc(1000, "u32", zero=False)
+    b.graph_begin()
+    try:
+        with pytest.raises(sm.ArgumentError):
+            b.alloc(16, "f32", zero=True)
+        with pytest.raises(sm.ArgumentError):
+            b._check(sm.lib().sm_zero(b._ctx, buf.handle, 2, 8))
+        b._check(sm.lib().sm_zero(b._ctx, buf.handle, 40, 400))  # words 10 .. 109
+    finally:
+        gid = b.graph_end()
+    for rep in range(3):
+        b.write(buf, np.full(1000, 0xA5A5A5A5 + rep, np.uint32))
+        b.graph_launch(gid)
+        got = b.read(buf)
+        assert np.all(got[10:110] == 0), rep
+        assert np.all(got[:10] == 0xA5A5A5A5 + rep) and np.all(got[110:] == 0xA5A5A5A5 + rep), rep
+    b.graph_free(gid)
+    b.free(buf)
