@@ -154,6 +154,23 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
                  int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,
                  uint64_t workspace_bytes);
 
+/* Allocation-free variant of sm_moe_layer for the decode path (no reference
+ * counterpart: it is for callers that cannot allocate, such as code under
+ * HIP graph capture or a serving loop that forbids hipMalloc). Same
+ * arguments and results as sm_moe_layer without the workspace: the decode
+ * scratch (router logits, per-group fixed-point activations, hidden rows)
+ * lives in a static device array of 2 MiB per GPU, held until the process
+ * ends. Runs the decode kernels only: tokens <= 24, and the shape's decode
+ * scratch must fit in 2 MiB (hidden 2048 / ff 512 / 512 experts / top-10
+ * needs 787 KiB at 24 tokens); larger requests fail with SM_E_ARG. Nothing
+ * is allocated (no hipMalloc / hipFree) and the scratch needs no clearing:
+ * every word a call reads, that call wrote first. Calls that overlap on one
+ * GPU (two streams or two contexts at once) share the array and race; calls
+ * in stream order do not. Refused while stage timing is enabled. */
+int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
+                        uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff,
+                        int experts, int topk, uint64_t Y, uint64_t ids, uint64_t weights);
+
 /* One block of a stacked decoder built on the MoE stage, the per-layer step
  * of the 48-layer stack (no single reference entry point; it composes
  * strata_norm mode 0 with scale 1, kernels/strata.cu:214-227, the MoE stage of

@@ -66,6 +66,7 @@ def lib():
             "sm_moe_dispatch": (i, [vp, u64, i, i, i, u64, u64, u64, u64, u64, u64]),
             "sm_moe_layer_workspace": (i, [i, i, i, i, i, pu64]),
             "sm_moe_layer": (i, [vp, u64, i, u64, u64, u64, u64, u64, u64, i, i, i, i, u64, u64, u64, u64, u64]),
+            "sm_moe_layer_static": (i, [vp, u64, i, u64, u64, u64, u64, u64, u64, i, i, i, i, u64, u64, u64]),
             "sm_moe_block_workspace": (i, [i, i, i, i, i, pu64]),
             "sm_moe_block": (i, [vp, u64, i, u64, ctypes.c_float, u64, u64, u64, u64, u64, u64, i, i, i, i, u64, u64,
                                  u64, u64, u64]),
@@ -284,6 +285,14 @@ class Backend:
                                        arena.handle, blob_stride, shared_blob.handle, Wsg.handle, width, ff, experts,
                                        topk, Y.handle, ids.handle, weights.handle, workspace.handle,
                                        workspace.nbytes))
+
+    def moe_layer_static(self, X, tokens, Wr, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
+                         weights, bias=None):
+        """sm_moe_layer without a workspace: the decode path on the library's
+        static device scratch (at most 24 tokens; nothing is allocated)."""
+        self._check(lib().sm_moe_layer_static(self._ctx, X.handle, tokens, Wr.handle, bias.handle if bias else 0,
+                                              arena.handle, blob_stride, shared_blob.handle, Wsg.handle, width, ff,
+                                              experts, topk, Y.handle, ids.handle, weights.handle))
 
     @staticmethod
     def moe_block_workspace_bytes(tokens, width, ff, experts, topk):

@@ -45,6 +45,8 @@ struct sm_ctx {
     // the events that mark their copies done.
     void *staging[2] = {nullptr, nullptr};
     hipEvent_t staged[2] = {nullptr, nullptr};
+    // Device address of this device's static decode scratch (sm_init).
+    void *scratch = nullptr;
 };
 
 namespace smi {
@@ -122,6 +124,12 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
                uint64_t ids, uint64_t weights, uint64_t workspace, uint64_t workspace_bytes,
                const BlockArgs *block = nullptr);
 uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int topk);
+// The static decode scratch of sm_moe_layer_static: its size, and the lookup
+// of its device address for ctx->device (sets ctx->scratch; called by sm_init
+// with that device current).
+constexpr uint64_t kStaticScratchBytes = 2ull << 20;
+constexpr int kMaxDevices = 64;
+int static_scratch_init(sm_ctx *ctx);
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
                 uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
                 int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,

@@ -30,6 +30,8 @@
 // load of a wave is issued before its arithmetic; reductions use DPP.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "internal.h"
 #include "strata_device.h"
 
@@ -721,7 +723,31 @@ DecodeWs decode_ws(int tokens, int width, int ff, int experts, int topk) {
 
 }  // namespace
 
+// Device scratch of the allocation-free decode entry (sm_moe_layer_static):
+// the decode workspace (logits, activation records, hidden rows) for any
+// call whose decode_ws() fits. Each GPU holds its own copy for the life of
+// the process; host code never passes this name to a kernel, only the
+// address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[smi::kStaticScratchBytes];
+
 namespace smi {
+
+int static_scratch_init(sm_ctx *ctx) {
+    // One lookup per device; every context on that device shares the array.
+    static std::mutex lock;
+    static void *by_device[kMaxDevices] = {};
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) return fail(ctx, SM_E_ARG, "device index out of range");
+    std::lock_guard<std::mutex> g(lock);
+    if (!by_device[ctx->device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(ctx, SM_E_HIP, "hipGetSymbolAddress(scratch) returned no address");
+        by_device[ctx->device] = p;
+    }
+    ctx->scratch = by_device[ctx->device];
+    return SM_OK;
+}
 
 uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int topk) {
     return decode_ws(tokens, width, ff, experts, topk).end;

@@ -123,6 +123,10 @@ int sm_init(int device, sm_ctx **out) {
         sm_shutdown(ctx);
         return SM_E_HIP;
     }
+    if (static_scratch_init(ctx) != SM_OK) {
+        sm_shutdown(ctx);
+        return SM_E_HIP;
+    }
     *out = ctx;
     return SM_OK;
 }
@@ -417,6 +421,38 @@ int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk,
     *bytes = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                          : moe_prefill_workspace(tokens, width, ff, experts, topk);
     return SM_OK;
+}
+
+int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
+                        uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
+                        int topk, uint64_t Y, uint64_t ids, uint64_t weights) {
+    if (!ctx) return SM_E_ARG;
+    if (int rc = check_geometry(ctx, tokens, width, ff, experts, topk)) return rc;
+    if (tokens > kDecodeMaxTokens)
+        return fail(ctx, SM_E_ARG, "the allocation-free entry runs the decode path: at most " +
+                                       std::to_string(kDecodeMaxTokens) + " tokens per call");
+    const uint64_t ws = moe_decode_workspace(tokens, width, ff, experts, topk);
+    if (ws > kStaticScratchBytes)
+        return fail(ctx, SM_E_ARG, "this shape needs " + std::to_string(ws) + " bytes of decode scratch; the static "
+                                   "scratch holds " + std::to_string(kStaticScratchBytes));
+    // Stage timing records host-side marks; keep this entry free of them.
+    if (ctx->stage_timing) return fail(ctx, SM_E_ARG, "disable stage timing before the allocation-free entry");
+    if (!ctx->scratch) return fail(ctx, SM_E_HIP, "static scratch not resolved for this device");
+    BlobLayout L = blob_layout(width, ff);
+    if (blob_stride < L.bytes || blob_stride % 256)
+        return fail(ctx, SM_E_ARG, "blob stride must be a multiple of 256 holding one blob");
+    if (int rc = need(ctx, arena, blob_stride * (uint64_t)(experts - 1) + L.bytes, "expert arena")) return rc;
+    if (int rc = need(ctx, shared_blob, L.bytes, "shared expert blob")) return rc;
+    if (int rc = need(ctx, X, (uint64_t)tokens * width * 4, "X")) return rc;
+    if (int rc = need(ctx, Y, (uint64_t)tokens * width * 4, "Y")) return rc;
+    if (int rc = need(ctx, Wr, (uint64_t)experts * width * 4, "router weights")) return rc;
+    if (int rc = need(ctx, Wsg, (uint64_t)width * 4, "shared gate weights")) return rc;
+    if (bias)
+        if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
+    if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
+    if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
+    return moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
+                      weights, (uint64_t)ctx->scratch, kStaticScratchBytes);
 }
 
 int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,

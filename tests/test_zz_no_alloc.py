@@ -1,0 +1,75 @@
+"""The allocation-free decode entry (sm_moe_layer_static) through the C ABI:
+its results are the bits of sm_moe_layer with a workspace, on two calls in a
+row, the second with fewer tokens; it allocates nothing, and it refuses
+shapes beyond its static scratch with a clear error."""
+import numpy as np
+import pytest
+
+import stratacuda_amd as sm
+from stratacuda_amd import workload as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.asarray(a).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def layers(backend):
+    made = {}
+    yield made
+    for lay in made.values():
+        lay.free()
+
+
+def _layer(backend, layers, width, ff):
+    if (width, ff) not in layers:
+        layers[(width, ff)] = wl.DeviceLayer(backend, layer=3, width=width, ff=ff)
+    return layers[(width, ff)]
+
+
+@pytest.mark.parametrize("width,ff,token_seq", [(2048, 512, (8, 1)), (2048, 512, (24, 3)), (2560, 640, (5, 1))])
+def test_static_entry_matches_workspace_entry(backend, layers, width, ff, token_seq):
+    b = backend
+    E, K = wl.EXPERTS, wl.TOPK
+    lay = _layer(b, layers, width, ff)
+    Tmax = max(token_seq)
+    X = b.alloc(Tmax * width, zero=False)
+    Y_ref, Y = b.alloc(Tmax * width), b.alloc(Tmax * width)
+    ids_ref, ids = b.alloc(Tmax * K, "i32"), b.alloc(Tmax * K, "i32")
+    w_ref, w = b.alloc(Tmax * K), b.alloc(Tmax * K)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(Tmax, width, ff, E, K))
+    for call, T in enumerate(token_seq):
+        print("static entry: width %d ff %d call %d tokens %d" % (width, ff, call, T), flush=True)
+        b.synth_normal(X, T * width, 4242 + 17 * call + T, wl.STREAM_INPUT, 1.0)
+        b.moe_layer(X, T, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, width, ff, E, K, Y_ref, ids_ref, w_ref,
+                    ws)
+        before = b.info()
+        b.moe_layer_static(X, T, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, width, ff, E, K, Y, ids, w)
+        b.sync()
+        after = b.info()
+        assert after["allocatedBytes"] == before["allocatedBytes"] and after["buffers"] == before["buffers"]
+        n, nk = T * width, T * K
+        assert np.array_equal(b.read(ids, count=nk), b.read(ids_ref, count=nk)), (call, T)
+        assert np.array_equal(bits(b.read(w, count=nk)), bits(b.read(w_ref, count=nk))), (call, T)
+        got, want = b.read(Y, count=n), b.read(Y_ref, count=n)
+        assert np.all(np.isfinite(got))
+        assert np.array_equal(bits(got), bits(want)), (call, T, float(np.abs(got - want).max()))
+    for buf in (X, Y_ref, Y, ids_ref, ids, w_ref, w, ws):
+        b.free(buf)
+
+
+def test_static_entry_refuses_what_does_not_fit(backend, layers):
+    b = backend
+    E, K = wl.EXPERTS, wl.TOPK
+    lay = _layer(b, layers, 2048, 512)
+    X, Y = b.alloc(25 * 2048), b.alloc(25 * 2048)
+    ids, w = b.alloc(25 * K, "i32"), b.alloc(25 * K)
+    with pytest.raises(sm.ArgumentError, match="at most 24 tokens"):
+        b.moe_layer_static(X, 25, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 512, E, K, Y, ids, w)
+    # 24 tokens of ff 2048 need 2.3 MB of hidden rows: beyond the 2 MiB scratch
+    with pytest.raises(sm.ArgumentError, match="static scratch holds"):
+        b.moe_layer_static(X, 24, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 2048, E, K, Y, ids, w)
+    for buf in (X, Y, ids, w):
+        b.free(buf)
