@@ -709,36 +709,61 @@ def main():
     median_us = rep_ms[len(rep_ms) // 2] * 1e3 / L
     mean_us = sum(rep_ms) * 1e3 / (len(rep_ms) * L)
 
-    # ---- per-kernel durations: graphs that run one decode stage each
+    # ---- per-kernel durations. One token at this geometry runs the single-
+    # launch layer (k_decode_fused): its duration per launch is the step time
+    # of the 48-step graph. The three-kernel decode path (stage 8 off) is
+    # timed beside it, stage by stage, from graphs that run one stage each.
     kernel_bytes = decode_kernel_bytes(W, F, E, K)
+    step_bytes = layer_bytes(W, F, E, K, 1, K)
+    fused = W == 2048 and F == 512 and K <= 10 and E <= 512
+    three_kernels = 0xffffffff & ~(1 << 8)
     kernels = {}
     reps = max(1, min(50, 2400 // L))
-    for stage, name in enumerate(["decode_route", "decode_gate_up", "decode_down_combine"]):
-        be.stage_select(1 << stage)
+
+    def timed_graph(mask, ev0, ev1):
+        be.stage_select(mask)
         gid = capture(all_layers)
         if not args.eager:
             be.stage_select()
         replay(gid)
         be.sync()
-        be.event_record(2)
+        be.event_record(ev0)
         for _ in range(reps):
             replay(gid)
-        be.event_record(3)
+        be.event_record(ev1)
         be.sync()
         be.stage_select()
-        us = be.event_elapsed_ms(2, 3) * 1e3 / (reps * L)
-        gbs = kernel_bytes[name] / (us * 1e-6) / 1e9
-        kernels[name] = {"avg_us": round(us, 3), "bytes_per_launch": kernel_bytes[name], "GB/s": round(gbs, 1),
-                         "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4)}
         release(gid)
-    dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
-    hip_kernel = {"decode_route": "k_decode_route", "decode_gate_up": "k_decode_gate_up",
-                  "decode_down_combine": "k_decode_down"}[dom]
-    roofline = {"bound": "hbm", "kernel": hip_kernel, "achieved": kernels[dom]["GB/s"], "peak": PEAK_HBM / 1e9,
-                "unit": "GB/s", "frac": kernels[dom]["frac_hbm"], "traffic": read_traffic(hip_kernel),
-                "bytes_per_launch": kernels[dom]["bytes_per_launch"], "avg_us": kernels[dom]["avg_us"]}
-    # whole step (all three kernels), against the per-token algorithmic bytes
-    step_bytes = layer_bytes(W, F, E, K, 1, K)
+        return be.event_elapsed_ms(ev0, ev1) * 1e3 / (reps * L)
+
+    if fused:
+        gbs = step_bytes / (mean_us * 1e-6) / 1e9
+        kernels["decode_fused"] = {"avg_us": round(mean_us, 3), "median_us": round(median_us, 3),
+                                   "bytes_per_launch": step_bytes, "GB/s": round(gbs, 1),
+                                   "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4),
+                                   "note": "one launch per step: the per-launch time includes the dispatch gap "
+                                           "between dependent launches in the graph"}
+    three = {}
+    for stage, name in enumerate(["decode_route", "decode_gate_up", "decode_down_combine"]):
+        us = timed_graph(1 << stage, 2, 3)
+        gbs = kernel_bytes[name] / (us * 1e-6) / 1e9
+        three[name] = {"avg_us": round(us, 3), "bytes_per_launch": kernel_bytes[name], "GB/s": round(gbs, 1),
+                       "frac_hbm": round(gbs * 1e9 / PEAK_HBM, 4)}
+    three["layer_us"] = round(timed_graph(three_kernels, 2, 3), 3)
+    if fused:
+        kernels["three_kernel_path"] = three
+        dom, hip_kernel = "decode_fused", "k_decode_fused"
+        dk = kernels[dom]
+    else:
+        kernels.update(three)
+        dom = max(("decode_route", "decode_gate_up", "decode_down_combine"), key=lambda k: three[k]["avg_us"])
+        hip_kernel = {"decode_route": "k_decode_route", "decode_gate_up": "k_decode_gate_up",
+                      "decode_down_combine": "k_decode_down"}[dom]
+        dk = three[dom]
+    roofline = {"bound": "hbm", "kernel": hip_kernel, "achieved": dk["GB/s"], "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": dk["frac_hbm"], "traffic": read_traffic(hip_kernel),
+                "bytes_per_launch": dk["bytes_per_launch"], "avg_us": dk["avg_us"]}
+    # whole step against the per-token algorithmic bytes
     step_s = gpu_ms * 1e-3 / args.steps
     layer_roof = {"bound": "hbm", "bytes_per_step": step_bytes, "achieved": round(step_bytes / step_s / 1e9, 1),
                   "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(step_bytes / step_s / PEAK_HBM, 4),
@@ -898,7 +923,9 @@ def main():
                 "uniforms (variance 1, |n| <= 6); random-init Q2 experts of the reference layout",
         "config": {"workload": "single MoE layer decode, T=1: hidden 2048, 512 experts, top-10 + shared, Q2 "
                                "(64-weight fp16-scale groups), 48 resident layers rotated per step",
-                   "tokens_per_step": 1, "layers_rotated": L, "execution": "HIP graph of 48 steps",
+                   "tokens_per_step": 1, "layers_rotated": L,
+                   "execution": "HIP graph of 48 steps, one launch per step (k_decode_fused)" if fused else
+                                "HIP graph of 48 steps, three launches per step",
                    "gpu_us_per_step": round(gpu_ms * 1e3 / args.steps, 3),
                    "median_us_per_step": round(median_us, 3), "mean_us_per_step_50_replays": round(mean_us, 3),
                    "timing": "value = steps / wall time of the timed region; median and mean over 50 separately "

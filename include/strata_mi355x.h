@@ -197,10 +197,13 @@ int sm_event_elapsed(sm_ctx *ctx, int start_slot, int end_slot, float *ms);
  * exposes counters through GpuBackend.info, src/backend.js:120). When enabled,
  * an event is recorded on the context's stream at every stage boundary;
  * sm_stage_report synchronises and returns, per stage, the accumulated
- * milliseconds and call counts since enabling (n >= 8 slots). Stages:
+ * milliseconds and call counts since enabling (n >= 9 slots). Stages:
  * 0 decode route, 1 decode gate/up, 2 decode down+combine, 3 prefill route
  * (router GEMM + top-k), 4 prefill dispatch, 5 prefill gate/up GEMM,
- * 6 prefill down GEMM, 7 prefill combine. Returns the number of stages. */
+ * 6 prefill down GEMM, 7 prefill combine, 8 the single-launch decode layer
+ * (one token at hidden 2048 / ff 512 / top-k <= 10; it runs when bits 0, 1,
+ * 2 and 8 are all set, otherwise stages 0-2 run as three kernels). Returns
+ * the number of stages. */
 int sm_stage_timing(sm_ctx *ctx, int enable);
 int sm_stage_report(sm_ctx *ctx, double *total_ms, uint64_t *calls, int n);
 /* Runs only the sm_moe_layer stages whose bit (1 << stage) is set; the

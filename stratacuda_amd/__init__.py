@@ -312,7 +312,7 @@ class Backend:
 
     # ------------------------------------------------------------ timing
     STAGES = ["decode_route", "decode_gate_up", "decode_down_combine", "prefill_route", "prefill_dispatch",
-              "prefill_gate_up_gemm", "prefill_down_gemm", "prefill_combine"]
+              "prefill_gate_up_gemm", "prefill_down_gemm", "prefill_combine", "decode_fused"]
 
     def stage_timing(self, enable=True):
         self._check(lib().sm_stage_timing(self._ctx, 1 if enable else 0))

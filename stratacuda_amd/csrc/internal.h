@@ -20,8 +20,9 @@ struct sm_ctx {
     std::map<uint64_t, uint64_t> buffers;  // handle (device address) -> bytes
     std::string error;
     hipEvent_t events[64] = {};
-    // Device words used by kernels that elect their last-arriving workgroup
-    // (route completion counters). Each kernel returns its counter to zero.
+    // kCounterWords device words (zeroed at sm_init): 254 and 255 the pack
+    // loader's and the index checks' flags; from kFusedSyncBase the fused
+    // decode layer's hand-off counters, go words and sticky fault word.
     uint32_t *counters = nullptr;
     uint64_t launches = 0, bytes_written = 0, bytes_read = 0, allocated = 0;
     // Stage timing (sm_stage_timing): events recorded at stage boundaries.
@@ -77,9 +78,14 @@ enum Stage {
     kStagePrefillGateUp = 5,
     kStagePrefillDown = 6,
     kStagePrefillCombine = 7,
-    kStageCount = 8
+    kStageDecodeFused = 8,  // the single-launch decode layer (one token)
+    kStageCount = 9
 };
 int stage_mark(sm_ctx *ctx, int stage);
+constexpr int kCounterWords = 4096;
+constexpr int kFusedSyncBase = 1024;
+// Index in ctx->counters of the fused decode layer's sticky fault word.
+uint32_t fused_fault_word();
 inline bool stage_on(const sm_ctx *ctx, int stage) { return (ctx->stage_mask >> stage) & 1u; }
 // Zero-fills n 32-bit words with a kernel (graph-capturable, unlike a memset node).
 int zero_words(sm_ctx *ctx, void *dst, uint64_t n);

@@ -704,6 +704,450 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
     down_combine(parts, s_w, sig, cin, Y, width, topk, resid != nullptr);
 }
 
+// ------------------------------------------------- fused single-token layer
+// The whole layer for one token in one launch of kFusedBlocks blocks of 8
+// waves (one block per CU), for hidden 2048 / ff 512. Two hand-offs between
+// blocks go through memory:
+//   A. router logits: waves 0 and 1 of every block compute two router rows
+//      (reference order) while waves 2-7 build the block's fixed-point
+//      activation records in LDS. Each logit is published as one 64-bit word
+//      holding the launch number beside the value, so a block's wave 0
+//      polls the 512 words themselves until every one is current (no flag
+//      or go word for this hand-off), and the block runs the exact top-k
+//      itself (no hand-off for the IDs).
+//   B. hidden rows: every wave computes kFusedRows of the 11 x 512 hidden
+//      rows (10 routed experts and the shared one), then loads the down
+//      codes of its block's 8 output rows for its slots. Every block waits
+//      for all hidden rows, forms its 8 output rows and combines them
+//      (kernels/strata.cu:360-365).
+// Cross-block data is written and read with agent-scope coherent accesses
+// (global/buffer accesses with the sc1 policy, which bypass the non-coherent
+// per-XCD L2 lines). Hand-off B: once its stores are complete, a block
+// writes the launch number into its own flag word; one collector wave reads
+// all 256 flags (16 bytes per lane) until every block is in and then
+// publishes the launch number in the go word, which the other blocks poll.
+// Plain stores and loads only: atomics on one address serialize (~14 ns
+// each on MI355X). The launch number is the go word's value when the block
+// starts plus one (the previous launch left it there), so nothing needs
+// resetting. Every wait gives up after kFusedSpinLimit
+// polls, setting a sticky fault word; the layer's outputs are then NaN.
+constexpr int kFusedBlocks = 256, kFusedWaves = 8;
+constexpr int kFusedRows = 3;  // hidden rows per wave: ceil(11 x 512 / 2048)
+constexpr int kFusedWidth = 2048, kFusedFF = 512, kFusedMaxTopk = 10;
+constexpr int kFusedCollector = kFusedBlocks - 1;  // block whose wave 7 collects the flags
+constexpr uint32_t kFusedSpinLimit = 1u << 20;
+// Word offsets in the synchronisation area (ctx->counters + kFusedSyncBase):
+// the flags of hand-off B (one word per block), then the go word and the
+// fault word on lines of their own.
+constexpr int kFusedFlagsB = 0, kFusedGoB = kFusedBlocks + 32, kFusedFaultWord = kFusedGoB + 32;
+// The tagged logits (two words per expert, 8-byte aligned), in the same area
+// so that only this kernel ever writes them: a stale tag is an earlier
+// launch's number, never the current one.
+constexpr int kFusedLogitWords = 512;
+constexpr int kFusedSyncWords = kFusedLogitWords + 2 * 512;
+
+struct FusedArgs {
+    const float *X, *Wr, *bias, *Wsg, *gamma;
+    const uint8_t *arena, *shared;
+    uint64_t stride, gu_scales, down_codes, down_scales;
+    float *Y, *weights, *gate, *hidden;
+    uint64_t *logits;  // (launch number << 32) | logit bits, per expert
+    int *ids;
+    uint32_t *sync;
+    float eps;
+    int experts, topk;
+};
+
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_coherent_u32(uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this wave's earlier stores are complete (at the coherence point
+// for the coherent ones) and keeps the compiler from moving memory accesses
+// across; what the wave does next is ordered after them.
+__device__ __forceinline__ void stores_complete() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+}
+__device__ __forceinline__ void loads_ordered() {
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+__device__ __forceinline__ void set_fault(uint32_t *fault) {
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_or(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 coherent bytes at byte offset `off` of a buffer (buffer load with the sc1
+// policy: served from the coherence point, not a stale L2 line).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+// Whole-wave wait for the go word to reach `launch`. Returns false (and sets
+// the sticky fault word) after kFusedSpinLimit polls.
+__device__ bool wait_go(uint32_t *go, uint32_t launch, uint32_t *fault) {
+    const uint32_t want = (uint32_t)__builtin_amdgcn_readfirstlane((int)launch);
+    for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+        const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)load_coherent_u32(go));
+        if ((int)(v - want) >= 0) {
+            loads_ordered();
+            return true;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    set_fault(fault);
+    return false;
+}
+// The collector: one wave reads the 256 flags of a phase (4 per lane) until
+// all hold `launch`, then publishes `launch` in the go word.
+__device__ bool collect(uint32_t *flags, uint32_t *go, uint32_t launch, uint32_t *fault) {
+    const uint32_t want = (uint32_t)__builtin_amdgcn_readfirstlane((int)launch);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(flags, (short)0, kFusedBlocks * 4, 0x00020000);
+    const uint32_t off = (uint32_t)(threadIdx.x & 63) * 16;
+    for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+        const uint4 f = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16));
+        const bool in = (int)(f.x - want) >= 0 && (int)(f.y - want) >= 0 && (int)(f.z - want) >= 0 &&
+                        (int)(f.w - want) >= 0;
+        if (__ballot(!in) == 0) {
+            loads_ordered();
+            if ((threadIdx.x & 63) == 0) __hip_atomic_store(go, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return true;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    set_fault(fault);
+    return false;
+}
+// Records in LDS sit kRecPitch words apart: 16 bytes more than a record, so
+// the 16-byte reads of lanes reading different groups fall in different
+// banks (a 256-byte pitch puts every lane in the same banks).
+constexpr int kRecPitch = XQ_WORDS + 4;
+// Record of group g from the block's LDS copy (the layout of load_xq).
+__device__ __forceinline__ void load_xq_lds(const uint32_t *rec, int g, XQ &q) {
+    const uint4 *p = (const uint4 *)(rec + g * kRecPitch);
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+        const uint4 v = p[i];
+        q.limb[4 * i] = v.x;
+        q.limb[4 * i + 1] = v.y;
+        q.limb[4 * i + 2] = v.z;
+        q.limb[4 * i + 3] = v.w;
+    }
+    q.unit = __builtin_bit_cast(float, rec[g * kRecPitch + 48]);
+    q.sum = (int)rec[g * kRecPitch + 49];
+}
+
+// Timeline hook, compiled in only with -DSM_FUSED_TRACE (profiling builds):
+// lane 0 of the calling wave records the real-time clock (100 MHz) at mark k
+// of its block.
+#ifdef SM_FUSED_TRACE
+__device__ uint64_t g_fused_trace[kFusedBlocks * 16];
+#define FUSED_MARK(k) \
+    do { if ((threadIdx.x & 63) == 0) g_fused_trace[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+// the same once the wave's outstanding loads are in (profiling builds only)
+#define FUSED_MARK_LOADED(k) \
+    do { __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8)); FUSED_MARK(k); } while (0)
+#else
+#define FUSED_MARK(k) \
+    do { } while (0)
+#define FUSED_MARK_LOADED(k) \
+    do { } while (0)
+#endif
+
+template <bool NORM>
+__global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs a) {
+    constexpr int G = kFusedWidth / 64, GD = kFusedFF / 64, ROW_BYTES = kFusedWidth / 4;
+    __shared__ __attribute__((aligned(16))) uint32_t s_rec[G * kRecPitch];
+    __shared__ uint64_t s_tab[32];
+    __shared__ sm::RouterScratch s_router;
+    __shared__ int s_ids[32];
+    __shared__ float s_w[32];
+    __shared__ float s_parts[(kFusedMaxTopk + 2) * 8];
+    __shared__ __attribute__((aligned(16))) float s_h[kFusedWaves][8 * DN_PITCH];
+    __shared__ uint32_t s_arrive;
+    __shared__ int s_ok;
+    __shared__ float s_logit[512];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.x, gw = b * kFusedWaves + wave;
+    const int half = lane >> 5, gl = lane & 31;
+    const int topk = a.topk, experts = a.experts, nslot = topk + 1;
+    uint32_t *fault = a.sync + kFusedFaultWord;
+    // This launch's number: the go word as the previous launch left it, plus
+    // one (consumed only by the tags, flags and waits).
+    const uint32_t launch = load_coherent_u32(a.sync + kFusedGoB) + 1u;
+    // LDS holds garbage at launch: the arrival counter is cleared before any
+    // wave can use it.
+    if (tid == 0) s_arrive = 0;
+    __syncthreads();
+    bool ok = true;
+    if (wave == 0) FUSED_MARK(0);
+
+    // ---- phase A. Waves 0-1: router row `row` (reference order). Waves 2-7:
+    // the block's activation records (group g by wave 2 + g % 6). Block 0's
+    // wave 2 also the shared gate logit. x is loaded first: vector loads
+    // return in order.
+    float xv[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) xv[j] = a.X[lane + 64 * j];
+    float xres = 0.0f;  // the block entry's residual for combine thread tid < 8
+    if (NORM) xres = a.X[min(b * 8 + (tid & 7), kFusedWidth - 1)];
+    const bool router = wave < 2;
+    const int row = b + kFusedBlocks * wave;
+    const bool gate_wave = b == 0 && wave == 2;
+    // One weight-row load site for the router row and the shared gate vector
+    // (the registers then have a single writer on every path).
+    const float *wsrc = router ? a.Wr + (int64_t)min(row, experts - 1) * kFusedWidth : gate_wave ? a.Wsg : nullptr;
+    float wv[G];
+    if (wsrc) {
+#pragma unroll
+        for (int j = 0; j < G; j++) wv[j] = __builtin_nontemporal_load(wsrc + lane + 64 * j);
+    }
+    const float rbias = router && a.bias ? a.bias[min(row, experts - 1)] : 0.0f;
+    if (NORM) {
+        float gv[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) gv[j] = a.gamma[lane + 64 * j];
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < G; j++) ss = ss + xv[j] * xv[j];
+        ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm::tree_sum64(ss)), 0));
+        const float inv = 1.0f / sqrtf(ss / (float)kFusedWidth + a.eps);
+#pragma unroll
+        for (int j = 0; j < G; j++) xv[j] = (xv[j] * inv) * gv[j];
+    }
+    sm::fill_exp_table(s_tab);
+
+    if (router) {
+        // logit = the reference's lane-strided sequential sum, then its tree
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < G; j++) sum = sum + wv[j] * xv[j];
+        sum = sm::tree_sum64(sum);
+        if (lane == 0 && row < experts) {
+            const float logit = a.bias ? sum + rbias : sum;
+            __hip_atomic_store(a.logits + row, ((uint64_t)launch << 32) | __builtin_bit_cast(uint32_t, logit),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (wave == 0) FUSED_MARK(2);
+    } else {
+        // records of groups g = wave - 2, wave + 4, ... (lane l of group g is xv[g])
+#pragma unroll
+        for (int q = 0; q < (G + 5) / 6; q++) {
+            const int g = wave - 2 + 6 * q;
+            if (g >= G) break;
+            float v = xv[0];
+#pragma unroll
+            for (int j = 1; j < G; j++) v = g == j ? xv[j] : v;
+            float unit;
+            int sum;
+            quantize_group_bytes(v, (uint8_t *)(s_rec + g * kRecPitch), unit, sum);
+            if (lane == 0) {
+                s_rec[g * kRecPitch + 48] = __builtin_bit_cast(uint32_t, unit);
+                s_rec[g * kRecPitch + 49] = (uint32_t)sum;
+            }
+        }
+        if (wave == 2) FUSED_MARK(1);
+        if (gate_wave) {
+            float gs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < G; j++) gs = gs + wv[j] * xv[j];
+            gs = sm::tree_sum64(gs);
+            if (lane == 0) store_coherent(a.gate, gs);
+        }
+    }
+
+    // ---- hand-off A: wave 0 polls the tagged logits until all are this
+    // launch's, and stages them in LDS; then every block routes the token
+    // itself (router_block512: one exponential per thread, wave 0 selects).
+    if (wave == 0) {
+        uint64_t t[8];
+        bool all = false;
+        for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                t[j] = __hip_atomic_load(a.logits + min(lane + 64 * j, experts - 1), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            bool mine = true;
+#pragma unroll
+            for (int j = 0; j < 8; j++) mine = mine && (uint32_t)(t[j] >> 32) == launch;
+            if (__ballot(!mine) == 0) {
+                all = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (!all) set_fault(fault);
+        ok = all;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            s_logit[lane + 64 * j] = lane + 64 * j < experts ? __builtin_bit_cast(float, (uint32_t)t[j]) : -3.402823e38f;
+        FUSED_MARK(3);
+        if (lane == 0) s_ok = ok;
+    }
+    __syncthreads();
+    ok = s_ok;
+    {
+        float lg[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) lg[j] = s_logit[lane + 64 * j];
+        sm::router_block512(lg, experts, topk, s_tab, s_router, s_ids);
+    }
+    if (wave == 0) {
+        FUSED_MARK(4);
+        sm::wave_lds_sync();
+        // weights = selected / max(sum of selected, 2^-14), sum in k order
+        float denom = 0.0f;
+        for (int k = 0; k < topk; ++k) denom = denom + s_router.val[k];
+        denom = fmaxf(denom, 0.00006103515625f);
+        if (lane < topk) {
+            const float wk = s_router.val[lane] / denom;
+            s_w[lane] = wk;
+            if (b == 0) {
+                a.ids[lane] = s_ids[lane];
+                a.weights[lane] = wk;
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) FUSED_MARK(5);
+
+    // ---- phase B: kFusedRows hidden rows of the 11 x 512 (item = slot x 512
+    // + row; the shared expert is slot topk).
+    const int rr = lane >> 3, g8 = lane & 7;
+    const int drow = b * 8 + rr;
+    {
+        uint4 c[kFusedRows];
+        uint32_t sb[kFusedRows];
+        bool rok[kFusedRows];
+#pragma unroll
+        for (int r = 0; r < kFusedRows; r++) {
+            const int item = min(gw * kFusedRows + r, nslot * kFusedFF - 1);
+            const int k = item / kFusedFF, j = item - k * kFusedFF;
+            const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, k < topk ? s_ids[k] : 0, k, topk, experts);
+            rok[r] = blob != nullptr;
+            blob = blob ? blob : a.shared;
+            const uint64_t wrow = 2 * (uint64_t)j + half;
+            c[r] = load_codes(blob + wrow * ROW_BYTES + gl * 16);
+            sb[r] = *(const uint16_t *)(blob + a.gu_scales + (wrow * G + gl) * 2);
+        }
+        if (wave == 0) FUSED_MARK_LOADED(10);
+        XQ q;
+        load_xq_lds(s_rec, gl, q);
+        float acc[kFusedRows];
+#pragma unroll
+        for (int r = 0; r < kFusedRows; r++) acc[r] = sm::half_bits(sb[r]) * dot64_q(c[r], q);
+        // row r's gate and up sums (lanes 31 and 63) go to lane r: one SiLU
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kFusedRows; r++) {
+            const float v = sm::half32_sum(acc[r]);
+            const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+            const float ur = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+            g = lane == r ? gr : g;
+            u = lane == r ? ur : u;
+        }
+        bool mine_ok = true;
+#pragma unroll
+        for (int r = 0; r < kFusedRows; r++) mine_ok = lane == r ? rok[r] : mine_ok;
+        const float h = mine_ok ? sm::silu(g, s_tab) * u : __builtin_nanf("");
+        const int item = gw * kFusedRows + lane;
+        if (lane < kFusedRows && item < nslot * kFusedFF) store_coherent(a.hidden + item, h);
+    }
+    stores_complete();
+    if (wave == 0) FUSED_MARK(6);
+    if (wave == 7) FUSED_MARK(7);
+    // the block's flag once all eight waves are done
+    if (lane == 0 && atomicAdd(&s_arrive, 1u) == kFusedWaves - 1)
+        __hip_atomic_store(a.sync + kFusedFlagsB + b, launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The down codes of this block's 8 output rows for the wave's slots
+    // (wave and wave + 8): in flight while the hidden rows come in.
+    uint4 dc[2];
+    uint32_t dsb[2];
+    bool dok[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int s = min(wave + kFusedWaves * q, nslot - 1);
+        const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, s < topk ? s_ids[s] : 0, s, topk, experts);
+        dok[q] = blob != nullptr;
+        blob = blob ? blob : a.shared;
+        dc[q] = load_codes(blob + a.down_codes + (uint64_t)drow * (kFusedFF / 4) + g8 * 16);
+        dsb[q] = *(const uint16_t *)(blob + a.down_scales + ((uint64_t)drow * GD + g8) * 2);
+    }
+    if (b == kFusedCollector && wave == kFusedWaves - 1 && ok)
+        collect(a.sync + kFusedFlagsB, a.sync + kFusedGoB, launch, fault);
+
+    // ---- phase B wait; then the block's 8 output rows.
+    if (wave == 0) {
+        if (ok) ok = wait_go(a.sync + kFusedGoB, launch, fault);
+        FUSED_MARK(8);
+    }
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+        a.hidden, (short)0, (int)((uint32_t)nslot * kFusedFF * 4), 0x00020000);
+    float *xh = s_h[wave];
+    // lane (rr, g8) brings values 8 rr .. 8 rr + 7 of hidden group g8 of each
+    // of the wave's slots; all loads issued before any is used (a slot past
+    // the last reads the last one again)
+    float4 hq[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int s = min(wave + kFusedWaves * q, nslot - 1);
+        const uint32_t off = (uint32_t)(s * kFusedFF + g8 * 64 + 8 * rr) * 4;
+        hq[q][0] = load16_coherent(hr, off);
+        hq[q][1] = load16_coherent(hr, off + 16);
+    }
+    const float shared_gate = load_coherent(a.gate);
+    if (wave == 0) FUSED_MARK_LOADED(11);
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int s = wave + kFusedWaves * q;
+        if (s >= nslot) break;
+        const float4 h0 = hq[q][0], h1 = hq[q][1];
+        float s8 = ((h0.x + h0.y) + (h0.z + h0.w)) + ((h1.x + h1.y) + (h1.z + h1.w));
+        s8 = s8 + sm::dpp_f32<0x128>(0.0f, s8);
+        {
+            const int u = __builtin_bit_cast(int, s8);
+            const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            s8 = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
+            const int w = __builtin_bit_cast(int, s8);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+            s8 = __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
+        }
+        *(float4 *)&xh[g8 * DN_PITCH + 8 * rr] = h0;
+        *(float4 *)&xh[g8 * DN_PITCH + 8 * rr + 4] = h1;
+        __builtin_amdgcn_wave_barrier();
+        float hv[64];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = *(const float4 *)&xh[g8 * DN_PITCH + 4 * i];
+            hv[4 * i] = v.x;
+            hv[4 * i + 1] = v.y;
+            hv[4 * i + 2] = v.z;
+            hv[4 * i + 3] = v.w;
+        }
+        __builtin_amdgcn_wave_barrier();
+        float v = dok[q] ? sm::half_bits(dsb[q]) * (dot64_4(dc[q], hv) - s8) : __builtin_nanf("");
+        v = sm::group8_sum(v);
+        if (g8 == 0) s_parts[s * 8 + rr] = v;
+    }
+    __syncthreads();
+    if (tid < 8) {
+        const int r = b * 8 + tid;
+        const float sig = sm::sigmoid(shared_gate, s_tab);
+        float value = s_parts[topk * 8 + tid] * sig;
+        for (int k = 0; k < topk; k++) value = value + s_parts[k * 8 + tid] * s_w[k];
+        if (load_coherent_u32(fault) != 0u) value = __builtin_nanf("");
+        a.Y[r] = NORM ? xres + value : value;
+    }
+    if (wave == 0) FUSED_MARK(9);
+}
+
 constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
@@ -749,6 +1193,23 @@ int static_scratch_init(sm_ctx *ctx) {
     return SM_OK;
 }
 
+uint32_t fused_fault_word() { return kFusedSyncBase + kFusedFaultWord; }
+static_assert(kFusedSyncBase + kFusedSyncWords <= kCounterWords, "fused decode sync area");
+static_assert((kFusedSyncBase + kFusedLogitWords) % 2 == 0, "tagged logits are 8-byte words");
+
+}  // namespace smi
+
+#ifdef SM_FUSED_TRACE
+extern "C" int sm_fused_trace_read(uint64_t *out, int n) {
+    if (n < kFusedBlocks * 16) return SM_E_ARG;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_fused_trace), sizeof(uint64_t) * kFusedBlocks * 16) == hipSuccess
+               ? SM_OK
+               : SM_E_HIP;
+}
+#endif
+
+namespace smi {
+
 uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int topk) {
     return decode_ws(tokens, width, ff, experts, topk).end;
 }
@@ -766,6 +1227,38 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
     float *hidden = (float *)(ws + w.hidden);
     const int blocks_per_expert = ceil_div(ff, GU_ROWS * GU_WAVES);
     uint32_t *xq = (uint32_t *)(ws + w.xq);
+    // One token at hidden 2048 / ff 512: the whole layer in one launch.
+    const uint32_t decode_stages = (1u << kStageDecodeRoute) | (1u << kStageDecodeGateUp) | (1u << kStageDecodeDown);
+    if (tokens == 1 && width == kFusedWidth && ff == kFusedFF && experts <= 2 * kFusedBlocks && topk <= kFusedMaxTopk &&
+        stage_on(ctx, kStageDecodeFused) && (ctx->stage_mask & decode_stages) == decode_stages) {
+        if (int rc = stage_mark(ctx, kStageDecodeFused)) return rc;
+        FusedArgs fa;
+        fa.X = (const float *)X;
+        fa.Wr = (const float *)Wr;
+        fa.bias = (const float *)bias;
+        fa.Wsg = (const float *)Wsg;
+        fa.gamma = gamma;
+        fa.arena = (const uint8_t *)arena;
+        fa.shared = (const uint8_t *)shared_blob;
+        fa.stride = blob_stride;
+        fa.gu_scales = L.gate_up_scales;
+        fa.down_codes = L.down_codes;
+        fa.down_scales = L.down_scales;
+        fa.Y = (float *)Y;
+        fa.weights = (float *)weights;
+        fa.logits = (uint64_t *)(ctx->counters + kFusedSyncBase + kFusedLogitWords);
+        fa.gate = (float *)(ws + w.gate);
+        fa.hidden = hidden;
+        fa.ids = (int *)ids;
+        fa.sync = ctx->counters + kFusedSyncBase;
+        fa.eps = eps;
+        fa.experts = experts;
+        fa.topk = topk;
+        const auto kf = gamma ? k_decode_fused<true> : k_decode_fused<false>;
+        kf<<<kFusedBlocks, 64 * kFusedWaves, 0, ctx->stream>>>(fa);
+        if (int rc = launched(ctx)) return rc;
+        return stage_mark(ctx, -1);
+    }
     // 1. router logits + shared gate logit + fixed-point activations
     if (stage_on(ctx, kStageDecodeRoute)) {
         if (int rc = stage_mark(ctx, kStageDecodeRoute)) return rc;

@@ -118,8 +118,9 @@ int sm_init(int device, sm_ctx **out) {
             return SM_E_HIP;
         }
     }
-    if (hipMalloc((void **)&ctx->counters, 256 * sizeof(uint32_t)) != hipSuccess ||
-        hipMemset(ctx->counters, 0, 256 * sizeof(uint32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    if (hipMalloc((void **)&ctx->counters, kCounterWords * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->counters, 0, kCounterWords * sizeof(uint32_t)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
         sm_shutdown(ctx);
         return SM_E_HIP;
     }
@@ -158,13 +159,22 @@ int sm_info(sm_ctx *ctx, char *buf, size_t cap) {
     if (!ctx || !buf) return SM_E_ARG;
     hipDeviceProp_t p;
     HIP_TRY(ctx, hipGetDeviceProperties(&p, ctx->device));
+    // The fused decode layer's sticky fault word (a wait that gave up); read
+    // synchronously, so only outside a capture (-1 while capturing).
+    long long faults = -1;
+    if (!ctx->capturing) {
+        uint32_t f = 0;
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        HIP_TRY(ctx, hipMemcpy(&f, ctx->counters + fused_fault_word(), sizeof(f), hipMemcpyDeviceToHost));
+        faults = f;
+    }
     int n = snprintf(buf, cap,
                      "{\"backend\":\"hip\",\"device\":%d,\"name\":\"%s\",\"arch\":\"%s\",\"computeUnits\":%d,"
                      "\"globalMemoryBytes\":%llu,\"dispatches\":%llu,\"allocatedBytes\":%llu,\"buffers\":%zu,"
-                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu}",
+                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu,\"fusedDecodeFault\":%lld}",
                      ctx->device, p.name, p.gcnArchName, p.multiProcessorCount, (unsigned long long)p.totalGlobalMem,
                      (unsigned long long)ctx->launches, (unsigned long long)ctx->allocated, ctx->buffers.size(),
-                     (unsigned long long)ctx->bytes_written, (unsigned long long)ctx->bytes_read);
+                     (unsigned long long)ctx->bytes_written, (unsigned long long)ctx->bytes_read, faults);
     return n;
 }
 

@@ -46,21 +46,22 @@ __constant__ static const uint64_t kExp2Tab[32] = {
 };
 // `tab` may point at a copy of kExp2Tab in LDS (a per-lane indexed load from
 // __constant__ memory goes through the vector memory path).
+// Branch-free: the main path runs on x clamped into the range where it
+// applies, and the special cases (the branches of the reference's expf:
+// -inf -> 0, inf / NaN -> x + x, overflow -> inf, underflow -> 0) are
+// selected afterwards, so a caller's independent exponentials interleave.
+// For every input the result equals the branching form's.
 __device__ __forceinline__ float expf_or(float x, const uint64_t *tab = kExp2Tab) {
     const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
     const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
     const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
     const double Shift = 0x1.8p+52;
-    uint32_t ux = __float_as_uint(x);
-    uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
-    double xd = (double)x;
+    const float kOver = 0x1.62e42ep6f, kUnder = -0x1.9fe368p6f;
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    const float xc = fminf(fmaxf(x, kUnder), kOver);  // NaN -> kUnder; its result is replaced below
+    double xd = (double)xc;
     double z = InvLn2N * xd;
     double kd = z + Shift;
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
@@ -73,7 +74,58 @@ __device__ __forceinline__ float expf_or(float x, const uint64_t *tab = kExp2Tab
     double y = C2 * r + 1.0;
     y = zz * r2 + y;
     y = y * s;
-    return (float)y;
+    float out = (float)y;
+    const bool special = abstop >= 0x42bu;
+    out = special && x < kUnder ? 0.0f : out;
+    out = special && x > kOver ? __uint_as_float(0x7f800000u) : out;
+    out = abstop >= 0x7f8u ? x + x : out;
+    out = ux == 0xff800000u ? 0.0f : out;
+    return out;
+}
+// N independent exponentials. Each main path is pinned (an empty asm that
+// consumes all N results) before its special cases are selected, so the
+// compiler cannot sink the N evaluations into separate conditional blocks
+// and they interleave (their table reads are issued together).
+template <int N>
+__device__ __forceinline__ void expf_or_n(const float (&x)[N], float (&out)[N], const uint64_t *tab = kExp2Tab) {
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double Shift = 0x1.8p+52;
+    const float kOver = 0x1.62e42ep6f, kUnder = -0x1.9fe368p6f;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float xc = fminf(fmaxf(x[i], kUnder), kOver);
+        double xd = (double)xc;
+        double z = InvLn2N * xd;
+        double kd = z + Shift;
+        uint64_t ki = (uint64_t)__double_as_longlong(kd);
+        kd = kd - Shift;
+        double r = z - kd;
+        uint64_t t = tab[ki % 32] + (ki << 47);
+        double s = __longlong_as_double((long long)t);
+        double zz = C0 * r + C1;
+        double r2 = r * r;
+        double y = C2 * r + 1.0;
+        y = zz * r2 + y;
+        y = y * s;
+        out[i] = (float)y;
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(out[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const uint32_t ux = __float_as_uint(x[i]);
+        const uint32_t abstop = (ux >> 20) & 0x7ffu;
+        const bool special = abstop >= 0x42bu;
+        float o = out[i];
+        o = special && x[i] < kUnder ? 0.0f : o;
+        o = special && x[i] > kOver ? __uint_as_float(0x7f800000u) : o;
+        o = abstop >= 0x7f8u ? x[i] + x[i] : o;
+        o = ux == 0xff800000u ? 0.0f : o;
+        out[i] = o;
+    }
 }
 // Fills an LDS copy of kExp2Tab (lanes 0-31 of every wave, one entry each,
 // all waves writing the same values) from values known at compile time: no
@@ -261,6 +313,18 @@ __device__ __forceinline__ float half32_sum(float v) {
     return v;
 }
 
+// Inclusive prefix sum over the 64 lanes (integers), by DPP: lane l gets
+// the sum of lanes 0..l.
+__device__ __forceinline__ int wave_scan_incl(int v) {
+    v = v + dpp_i32<0x111>(0, v);  // row_shr:1
+    v = v + dpp_i32<0x112>(0, v);  // row_shr:2
+    v = v + dpp_i32<0x114>(0, v);  // row_shr:4
+    v = v + dpp_i32<0x118>(0, v);  // row_shr:8
+    v = v + dpp_i32<kDppRowBcast15, 0xa>(0, v);
+    v = v + dpp_i32<kDppRowBcast31, 0xc>(0, v);
+    return v;
+}
+
 // -------------------------------------------------------- synthetic data
 // Counter-based generator for the seeded synthetic workloads (the same
 // definition is restated independently in the CPU oracle):
@@ -302,6 +366,13 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     uint32_t half = ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1fffu;
     if (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) half++;
     return (uint16_t)(sign | half);
+}
+
+// Population count of a wave mask as a 32-bit int: two 32-bit counts keep
+// the comparison that follows on the scalar unit (a 64-bit count compared
+// with a constant becomes a vector compare and a round trip through VALU).
+__device__ __forceinline__ int popc64(unsigned long long m) {
+    return __builtin_popcount((uint32_t)m) + __builtin_popcount((uint32_t)(m >> 32));
 }
 
 // Selection keys for the reference's top-k rounds (kernels/strata.cu:252-265).
@@ -352,7 +423,7 @@ __device__ __forceinline__ void select_rounds(const int (&key)[8], int experts, 
         if (top != 0u) {
             const unsigned long long tied = __ballot(head == top);
             const int id = lane + 64 * (7 - (int)(P[0] & 7u));
-            if (__popcll(tied) == 1) winner = __builtin_amdgcn_readlane(id, __ffsll((long long)tied) - 1);
+            if (popc64(tied) == 1) winner = __builtin_amdgcn_readlane(id, __ffsll((long long)tied) - 1);
             else winner = wave_min_i32(head == top ? id : 0x7fffffff);
             value = __builtin_bit_cast(float, top ^ 0x80000000u);
             lowest_picked = min(lowest_picked, winner);
@@ -431,8 +502,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 struct RouterScratch {
     float p[512];
     float red[4];
-    uint64_t cand[128];  // 64 candidates + one discard slot per lane
-    int ids[32];
+    alignas(16) uint64_t cand[128];  // up to 64 candidates, zeros after the last (read 8 at a time)
     float val[32];
 };
 
@@ -446,17 +516,20 @@ struct RouterScratch {
 // bits. The entries with key >= T are gathered in LDS (one per lane) and
 // each is ranked against the others. With more than 64 such entries (heavy
 // ties), or fewer than topK lanes holding a probability >= 0 (NaN routing
-// input), the rounds of select_rounds run instead.
+// input), the rounds of select_rounds run instead. Results: the IDs in
+// s_ids[0, topK) and the selected probabilities in x.val[0, topK) (LDS).
 __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, int topK, RouterScratch &x,
-                                              int *s_ids, float &mine) {
+                                              int *s_ids) {
     const int lane = threadIdx.x & 63;
+    float mine;
     uint32_t hk = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) hk = max(hk, (uint32_t)key[j] ^ 0x80000000u);
     // Every valid entry (p >= 0) has a key >= 2^31 here; fewer than topK
     // lanes with one means NaN routing input or topK > 64.
-    if (__popcll(__ballot(hk >= 0x80000000u)) < topK) {
+    if (popc64(__ballot(hk >= 0x80000000u)) < topK) {
         select_rounds(key, experts, topK, s_ids, mine);
+        if (lane < topK) x.val[lane] = mine;
         return;
     }
     // Bits 29..16 of T (p <= 1 keeps bit 30 clear). Any T at or below the
@@ -467,52 +540,54 @@ __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, 
 #pragma unroll
     for (int b = 29; b >= 16; b--) {
         const uint32_t c = T | (1u << b);
-        if (__popcll(__ballot(hk >= c)) >= topK) T = c;
+        if (popc64(__ballot(hk >= c)) >= topK) T = c;
     }
+    // Candidates: entries with key >= T. Lane l's candidates go to cand[]
+    // from its exclusive prefix (a lane scan of the per-lane counts, all on
+    // the vector unit); the slots after the last hold 0, below every
+    // candidate (a candidate's key has its top bit set).
     uint64_t Q[8];
     bool in[8];
-    unsigned long long mask[8];
-    int count = 0;
+    int pos[8], n = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const uint32_t k = (uint32_t)key[j] ^ 0x80000000u;
         Q[j] = ((uint64_t)k << 9) | (uint64_t)(511 - (lane + 64 * j));
         in[j] = k >= T;
-        mask[j] = __ballot(in[j]);
-        count += __popcll(mask[j]);
+        pos[j] = n;
+        n += in[j] ? 1 : 0;
     }
+    const int incl = wave_scan_incl(n);
+    const int count = __builtin_amdgcn_readlane(incl, 63);
     if (count > 64) {
         select_rounds(key, experts, topK, s_ids, mine);
+        if (lane < topK) x.val[lane] = mine;
         return;
     }
-    // Gather: candidate i goes to cand[i]; entries below T to the lane's
-    // discard slot (no branches).
-    int base = 0;
+    x.cand[lane] = 0ull;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int below =
-            __builtin_amdgcn_mbcnt_hi((uint32_t)(mask[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask[j], 0));
-        x.cand[in[j] ? base + below : 64 + lane] = Q[j];
-        base += __popcll(mask[j]);
-    }
+    for (int j = 0; j < 8; j++)
+        if (in[j]) x.cand[incl - n + pos[j]] = Q[j];
     wave_lds_sync();
-    // Candidate `lane` against every candidate, read from its lane.
-    const uint64_t q = lane < count ? x.cand[lane] : 0ull;
+    // Candidate `lane` against every candidate: 8 at a time through
+    // broadcast 16-byte LDS reads (every lane reads the same address).
+    const uint64_t q = x.cand[lane];
     int rank = 0;
-    for (int c = 0; c < count; c++) {
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)q, c);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(q >> 32), c);
-        rank += (((uint64_t)hi << 32) | lo) > q ? 1 : 0;
+    for (int c = 0; c < count; c += 8) {
+        const uint4 *src = (const uint4 *)&x.cand[c];
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = src[u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint64_t a = ((uint64_t)v[u].y << 32) | v[u].x, b = ((uint64_t)v[u].w << 32) | v[u].z;
+            rank += (a > q ? 1 : 0) + (b > q ? 1 : 0);
+        }
     }
+    // the round-`rank` winner: its ID and probability straight into place
     if (lane < count && rank < topK) {
-        x.ids[rank] = 511 - (int)(q & 511u);
+        s_ids[rank] = 511 - (int)(q & 511u);
         x.val[rank] = __builtin_bit_cast(float, (uint32_t)(q >> 9) ^ 0x80000000u);
-    }
-    wave_lds_sync();
-    mine = 0.0f;
-    if (lane < topK) {
-        s_ids[lane] = x.ids[lane];
-        mine = x.val[lane];
     }
 }
 
@@ -534,9 +609,10 @@ __device__ __forceinline__ void router_load(const float *Logits, int experts, fl
 #pragma unroll
     for (int j = 0; j < 8; j++) l[j] = lane + 64 * j < experts ? v[j] : -3.402823e38f;
 }
+__device__ __forceinline__ void router_select_lds(int experts, int topK, RouterScratch &s, int *s_ids);
 __device__ __forceinline__ void router_block(const float (&l)[8], int experts, int topK, const uint64_t *s_tab,
                                              RouterScratch &s, int *s_ids) {
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int e0 = tid, e1 = tid + 256;
     // fmaxf returns one of its operands, so the order of the maximum does
@@ -555,10 +631,42 @@ __device__ __forceinline__ void router_block(const float (&l)[8], int experts, i
         }
     // Entries past `experts` hold +0: adding them to the (non-negative or
     // NaN) sums below changes nothing, so wave 0 reads all eight at once.
-    s.p[e0] = e0 < experts ? expf_or(l0 - mx, s_tab) : 0.0f;
-    s.p[e1] = e1 < experts ? expf_or(l1 - mx, s_tab) : 0.0f;
+    const float d[2] = {l0 - mx, l1 - mx};
+    float ex[2];
+    expf_or_n<2>(d, ex, s_tab);
+    s.p[e0] = e0 < experts ? ex[0] : 0.0f;
+    s.p[e1] = e1 < experts ? ex[1] : 0.0f;
     __syncthreads();
     if (wave != 0) return;
+    router_select_lds(experts, topK, s, s_ids);
+}
+// The same with 512 threads (8 waves): thread t forms expert t's exponential.
+// Needs blockDim.x == 512 and experts <= 512.
+__device__ __forceinline__ void router_block512(const float (&l)[8], int experts, int topK, const uint64_t *s_tab,
+                                                RouterScratch &s, int *s_ids) {
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float mx = l[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) mx = fmaxf(mx, l[j]);
+    mx = wave_max(mx);
+    wave_lds_sync();  // this wave's copy of the exp table is in LDS
+    float lw = l[0];  // expert tid = lane + 64 wave
+#pragma unroll
+    for (int j = 1; j < 8; j++) lw = wave == j ? l[j] : lw;
+    const float d[1] = {lw - mx};
+    float ex[1];
+    expf_or_n<1>(d, ex, s_tab);
+    s.p[tid] = tid < experts ? ex[0] : 0.0f;
+    __syncthreads();
+    if (wave != 0) return;
+    router_select_lds(experts, topK, s, s_ids);
+}
+// Wave 0's part of router_block / router_block512: the reference sum of the
+// probabilities in s.p, the selection, and the selected probabilities in
+// s.val[0, topK).
+__device__ __forceinline__ void router_select_lds(int experts, int topK, RouterScratch &s, int *s_ids) {
+    const int lane = threadIdx.x & 63;
     float p[8];
     float sum = 0.0f;
 #pragma unroll
@@ -570,11 +678,9 @@ __device__ __forceinline__ void router_block(const float (&l)[8], int experts, i
     int key[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) key[j] = select_key(p[j] * inv, lane + 64 * j < experts);
-    float mine;
-    select_ranked(key, experts, topK, s, s_ids, mine);
-    // The selected probabilities, for router_weights once the block has
-    // issued its expert loads (the IDs alone gate those).
-    if (lane < topK) s.val[lane] = mine;
+    // IDs into s_ids, selected probabilities into s.val (for router_weights
+    // once the block has issued its expert loads: the IDs alone gate those)
+    select_ranked(key, experts, topK, s, s_ids);
 }
 
 }  // namespace sm

@@ -1,0 +1,167 @@
+"""The single-launch decode layer (one token, hidden 2048 / ff 512) against
+the three-kernel decode path and the CPU oracle: the same bits as the three
+kernels (both compute every product and sum in the same order), routing
+bit-exact with the oracle, and the hand-off counters back at zero after
+every launch (many launches in a row, across layers, from a graph)."""
+import numpy as np
+import pytest
+
+from conftest import tol_ok
+from stratacuda_amd import workload as wl
+
+pytestmark = pytest.mark.gpu
+
+ALL = 0xffffffff
+THREE_KERNELS = ALL & ~(1 << 8)  # stage 8 off: the decode stages as three launches
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def two_layers(backend):
+    ls = [wl.DeviceLayer(backend, layer=l) for l in (5, 6)]
+    yield ls
+    for l in ls:
+        l.free()
+
+
+def run_layer(b, lay, X, Y, ids, w, ws, mask, block=False, Hout=None, E=wl.EXPERTS, K=wl.TOPK, bias=None):
+    W, F = wl.WIDTH, wl.FF
+    b.stage_select(mask)
+    try:
+        if block:
+            b.moe_block(X, 1, lay.gamma, 1e-6, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K,
+                        Hout, ids, w, ws, bias=bias)
+        else:
+            b.moe_layer(X, 1, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, Y, ids, w, ws,
+                        bias=bias)
+    finally:
+        b.stage_select()
+
+
+@pytest.mark.parametrize("block", [False, True])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_fused_matches_three_kernels(backend, two_layers, block, seed):
+    b = backend
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    lay = two_layers[seed % 2]
+    X = b.alloc(W, zero=False)
+    b.synth_normal(X, W, 600 + seed, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_block_workspace_bytes(1, W, F, E, K))
+    outs = []
+    for mask in (ALL, THREE_KERNELS):
+        Y, ids, w = b.alloc(W), b.alloc(K, "i32"), b.alloc(K)
+        run_layer(b, lay, X, Y, ids, w, ws, mask, block=block, Hout=Y)
+        outs.append((b.read(Y), b.read(ids), b.read(w)))
+    (y0, i0, w0), (y1, i1, w1) = outs
+    assert np.array_equal(i0, i1)
+    assert np.array_equal(bits(w0), bits(w1))
+    assert np.all(np.isfinite(y0))
+    assert np.array_equal(bits(y0), bits(y1)), float(np.abs(y0 - y1).max())
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+def test_fused_block_in_place(backend, two_layers):
+    # Hout == H: every block reads all of H before any block writes its rows.
+    b = backend
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    lay = two_layers[0]
+    H1, H2 = b.alloc(W, zero=False), b.alloc(W, zero=False)
+    b.synth_normal(H1, W, 77, wl.STREAM_INPUT, 1.0)
+    b.copy(H1, H2)
+    Hout = b.alloc(W)
+    ws = b.alloc_bytes(b.moe_block_workspace_bytes(1, W, F, E, K))
+    ids, w = b.alloc(K, "i32"), b.alloc(K)
+    run_layer(b, lay, H1, None, ids, w, ws, THREE_KERNELS, block=True, Hout=Hout)
+    run_layer(b, lay, H2, None, ids, w, ws, ALL, block=True, Hout=H2)
+    assert np.array_equal(bits(b.read(H2)), bits(b.read(Hout)))
+
+
+def test_many_launches_in_a_row(backend, two_layers):
+    # 96 launches back to back (layers alternating, inputs changing), then the
+    # same sequence replayed from a graph three times: each launch's result
+    # equals the three-kernel result for its input; no wait ever gave up.
+    b = backend
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    n = 96
+    X = b.alloc(n * W, zero=False)
+    b.synth_normal(X, n * W, 991, wl.STREAM_INPUT, 1.0)
+    xs = [b.alloc(W, zero=False) for _ in range(n)]
+    for i in range(n):
+        b.copy(X, xs[i], W, i * W, 0)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, W, F, E, K))
+    ref = []
+    for i in range(n):
+        Y, ids, w = b.alloc(W), b.alloc(K, "i32"), b.alloc(K)
+        run_layer(b, two_layers[i % 2], xs[i], Y, ids, w, ws, THREE_KERNELS)
+        ref.append((Y, ids, w))
+    outs = [(b.alloc(W), b.alloc(K, "i32"), b.alloc(K)) for _ in range(n)]
+
+    def sequence():
+        for i in range(n):
+            run_layer(b, two_layers[i % 2], xs[i], *outs[i], ws, ALL)
+
+    def check(tag):
+        for i in range(n):
+            assert np.array_equal(bits(b.read(outs[i][0])), bits(b.read(ref[i][0]))), (tag, i)
+            assert np.array_equal(b.read(outs[i][1]), b.read(ref[i][1])), (tag, i)
+        for o in outs:
+            b.zero(o[0])
+
+    sequence()
+    check("eager")
+    b.graph_begin()
+    sequence()
+    gid = b.graph_end()
+    for rep in range(3):
+        b.graph_launch(gid)
+        b.sync()
+        check("replay %d" % rep)
+    b.graph_free(gid)
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+@pytest.mark.parametrize("experts,topk", [(512, 4), (300, 10), (130, 7), (512, 1)])
+def test_fused_other_routing_shapes(backend, oracle, experts, topk):
+    # Fewer experts (router rows past `experts` idle) and smaller top-k
+    # (waves past topk x 512 hidden rows idle), against the oracle.
+    b = backend
+    W, F = wl.WIDTH, wl.FF
+    lay = wl.DeviceLayer(b, layer=9, experts=experts)
+    X = b.alloc(W, zero=False)
+    b.synth_normal(X, W, 4000 + experts + topk, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, W, F, experts, topk))
+    Y, ids, w = b.alloc(W), b.alloc(topk, "i32"), b.alloc(topk)
+    Y3, ids3, w3 = b.alloc(W), b.alloc(topk, "i32"), b.alloc(topk)
+    run_layer(b, lay, X, Y, ids, w, ws, ALL, E=experts, K=topk)
+    run_layer(b, lay, X, Y3, ids3, w3, ws, THREE_KERNELS, E=experts, K=topk)
+    got_ids = b.read(ids)
+    host = wl.host_layer(oracle, 9, experts=experts, expert_ids=list(got_ids))
+    eY, eids, ew = oracle.moe_layer(b.read(X), 1, host["Wr"], host["arena"], host["stride"], host["shared"],
+                                    host["Wsg"], W, F, experts, topk)
+    lay.free()
+    assert np.array_equal(got_ids, eids)
+    assert np.array_equal(bits(b.read(w)), bits(ew))
+    got = b.read(Y)
+    assert tol_ok(got, eY), float(np.abs(got - eY).max())
+    assert np.array_equal(bits(got), bits(b.read(Y3)))
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+def test_fused_stage_timing(backend, two_layers):
+    # With stage timing on, the single launch is reported as stage 8.
+    b = backend
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    X = b.alloc(W, zero=False)
+    b.synth_normal(X, W, 5, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, W, F, E, K))
+    Y, ids, w = b.alloc(W), b.alloc(K, "i32"), b.alloc(K)
+    b.stage_timing(True)
+    for _ in range(4):
+        run_layer(b, two_layers[0], X, Y, ids, w, ws, ALL)
+    rep = b.stage_report()
+    b.stage_timing(False)
+    assert rep["decode_fused"][1] == 4
+    assert rep["decode_route"][1] == 0
