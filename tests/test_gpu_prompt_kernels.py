@@ -102,6 +102,36 @@ def test_gdn_gates_and_gdn_batch(backend, oracle, dim, kh, vh, tokens):
         same(backend.read(sb), state)
 
 
+@pytest.mark.parametrize("dim,kh,vh,tokens,alias", [(160, 2, 4, 3, False), (16, 2, 4, 3, True),
+                                                    (160, 2, 3, 5, True)])
+def test_gdn_batch_general_kernel(backend, oracle, dim, kh, vh, tokens, alias):
+    # The kernel for a state column longer than 128 values, or a State that
+    # another argument aliases (here Y: each thread's token outputs overwrite
+    # rows of its own column, as in the reference's loop), bit-exact with the
+    # oracle over two chunks.
+    rng = np.random.default_rng(dim + 7 * tokens + alias)
+    decay = (0.9 + 0.1 * rng.random(vh * tokens)).astype(np.float32)
+    strength = rng.random(vh * tokens).astype(np.float32)
+    state = rng.normal(0, 0.1, dim * vh * dim).astype(np.float32)
+    sb = backend.alloc(state)
+    y = sb if alias else backend.alloc(vh * dim * tokens)
+    db, stb = backend.alloc(decay), backend.alloc(strength)
+    for chunk in range(2):
+        q = (rng.normal(0, 1, kh * dim * tokens) / np.sqrt(dim)).astype(np.float32)
+        k = (rng.normal(0, 1, kh * dim * tokens) / np.sqrt(dim)).astype(np.float32)
+        v = rng.normal(0, 1, vh * dim * tokens).astype(np.float32)
+        backend.run("strata_gdn_batch", {"State": sb, "Q": backend.alloc(q), "K": backend.alloc(k),
+                                         "V": backend.alloc(v), "Decay": db, "Beta": stb, "Y": y,
+                                         "dim": dim, "keyHeads": kh, "valueHeads": vh, "tokens": tokens},
+                    grid(vh * dim))
+        if alias:
+            # the oracle's loop with Y = State, as the GPU call had it
+            oracle.lib().or_gdn_batch(state, q, k, v, decay, strength, state, dim, kh, vh, tokens)
+        else:
+            same(backend.read(y), oracle.gdn_batch(state, q, k, v, decay, strength, dim, kh, vh, tokens))
+        same(backend.read(sb), state)
+
+
 @pytest.mark.parametrize("dim,rotary,heads,tokens", [(8, 8, 4, 3), (256, 64, 24, 5)])
 def test_rope_batch(backend, oracle, dim, rotary, heads, tokens):
     rng = np.random.default_rng(dim)

@@ -2,9 +2,10 @@
 on the GPU, teacher-forced against the CPU oracle: every layer's routing is
 recomputed by the oracle from the GPU's own input to that layer, so routed
 IDs, their order and the routing weights must match bit for bit at every
-layer, and every layer's output within |a - e| <= 1e-4 + 1e-3 |e| (the f32
-trajectory itself is not bit-exact: the fused expert products only meet the
-tolerance)."""
+layer (all 128 configured steps at batch 1, every 8th at batch 32), and
+every layer's output within |a - e| <= 1e-4 + 1e-3 |e| (the f32 trajectory
+itself is not bit-exact: the fused expert products only meet the
+tolerance; tests/test_gpu_stack_free.py follows the two trajectories apart)."""
 import numpy as np
 import pytest
 
@@ -20,12 +21,40 @@ def same_bits(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
+STEPS = 128  # the configured decode length
+
+
 @pytest.fixture(scope="module")
 def stack_layers(backend):
     layers = [wl.DeviceLayer(backend, l) for l in range(LAYERS)]
     yield layers
     for lay in layers:
         lay.free()
+
+
+@pytest.fixture(scope="module")
+def router_weights(backend, stack_layers):
+    """Host copies of every layer's router matrix and RMSNorm gamma."""
+    return [(backend.read(lay.Wr), backend.read(lay.gamma)) for lay in stack_layers]
+
+
+def oracle_routing(oracle, h, tokens, Wr, gamma):
+    """strata_norm mode 0, the router projection and strata_router, in the
+    reference's order, for `tokens` rows of the layer input h."""
+    xn = oracle.norm(h, gamma, wl.WIDTH, tokens, 1, 0, 1e-6, 1.0)
+    logits = oracle.project(xn, Wr, wl.WIDTH, wl.EXPERTS, tokens)
+    return oracle.router(logits, wl.EXPERTS, wl.TOPK, tokens)
+
+
+def teacher_forced_routing(backend, oracle, st, router_weights, tokens):
+    """Every layer's routed IDs and weights against the oracle's routing of
+    the GPU's own input to that layer; returns the number of layers checked."""
+    for l in range(LAYERS):
+        Wr, gamma = router_weights[l]
+        rids, rw = oracle_routing(oracle, backend.read(st.H[l]), tokens, Wr, gamma)
+        assert np.array_equal(backend.read(st.ids[l]), rids), "layer %d routing differs" % l
+        assert same_bits(backend.read(st.w[l]), rw), "layer %d routing weights differ" % l
+    return LAYERS
 
 
 def check_layer(backend, oracle, st, l, rows):
@@ -53,6 +82,35 @@ def test_stack_decode_batch1_every_layer(backend, oracle, stack_layers):
             assert np.all(np.isfinite(backend.read(st.output())))
             for l in range(LAYERS):
                 check_layer(backend, oracle, st, l, [0])
+    finally:
+        st.free()
+
+
+def test_stack_decode_batch1_all_steps_routing(backend, oracle, stack_layers, router_weights):
+    # The configured 128 decode steps at batch 1, each from its own seeded
+    # N(0, 1) input: every layer's routing, teacher-forced, bit-exact.
+    st = wl.DeviceStack(backend, layers=stack_layers, tokens=1, trace=True)
+    try:
+        checked = 0
+        for step in range(STEPS):
+            st.input(wl.BASE_SEED + 5000 + step)
+            st.step()
+            assert np.all(np.isfinite(backend.read(st.output()))), step
+            checked += teacher_forced_routing(backend, oracle, st, router_weights, 1)
+        assert checked == STEPS * LAYERS
+    finally:
+        st.free()
+
+
+def test_stack_batch32_strided_steps_routing(backend, oracle, stack_layers, router_weights):
+    # Every 8th of the 128 batch-32 steps: all 32 tokens' routing at every
+    # layer, teacher-forced, bit-exact.
+    st = wl.DeviceStack(backend, layers=stack_layers, tokens=32, trace=True)
+    try:
+        for step in range(0, STEPS, 8):
+            st.input(wl.BASE_SEED + 9000 + step)
+            st.step()
+            teacher_forced_routing(backend, oracle, st, router_weights, 32)
     finally:
         st.free()
 
