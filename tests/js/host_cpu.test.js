@@ -13,39 +13,11 @@ import {Ops} from '../../stratacuda_amd/src/ops.js';
 import {WeightResidency, expertKey} from '../../stratacuda_amd/src/residency.js';
 import {SyntheticStore, blobLayout} from '../../stratacuda_amd/src/store.js';
 import {MoeStage} from '../../stratacuda_amd/src/moe.js';
+import {fakeAddon as makeFakeAddon} from './fake_addon.js';
 
 const real = loadAddon();
 
-function fakeAddon() {
-    const mem = new Map(), calls = [];
-    let next = 4096;
-    return {
-        calls, mem,
-        init: () => ({ctx: true}),
-        shutdown: () => {},
-        info: () => JSON.stringify({device: 'stand-in'}),
-        alloc: (ctx, bytes) => { const h = next; next += Math.max(256, Math.ceil(bytes / 256) * 256); mem.set(h, new Uint8Array(bytes)); return h; },
-        free: (ctx, h) => { if (!mem.delete(h)) throw Error('double free'); },
-        write: (ctx, h, off, data) => {
-            const src = ArrayBuffer.isView(data) ? new Uint8Array(data.buffer, data.byteOffset, data.byteLength) : new Uint8Array(data);
-            mem.get(h).set(src, off);
-        },
-        read: (ctx, h, off, n) => mem.get(h).slice(off, off + n).buffer,
-        copy: (ctx, s, so, d, dof, n) => mem.get(d).set(mem.get(s).subarray(so, so + n), dof),
-        zero: (ctx, h, off, n) => mem.get(h).fill(0, off, off + n),
-        sync: () => {},
-        signature: name => real.signature(name),
-        kernels: () => real.kernels(),
-        run: (ctx, name, groups, slots) => calls.push({name, groups, slots}),
-        moeWorkspace: (...a) => real.moeWorkspace(...a),
-        moeLayer: (ctx, ...args) => calls.push({name: 'moeLayer', args}),
-        moeBlockWorkspace: (...a) => real.moeBlockWorkspace(...a),
-        moeBlock: (ctx, ...args) => calls.push({name: 'moeBlock', args}),
-        synthBlobs: (ctx, ...args) => calls.push({name: 'synthBlobs', args}),
-        synthNormal: (ctx, ...args) => calls.push({name: 'synthNormal', args}),
-        synthUniformPm: (ctx, ...args) => calls.push({name: 'synthUniformPm', args}),
-    };
-}
+const fakeAddon = () => makeFakeAddon(real);
 
 test('the addon exports every entry of the C ABI it wraps', () => {
     for (const f of ['init', 'shutdown', 'lastError', 'info', 'alloc', 'free', 'size', 'write', 'read', 'copy', 'zero',

@@ -3,7 +3,8 @@ residency.js, store.js, moe.js) under Node, through the Node-API addon.
 
 CPU: tests/js/host_cpu.test.js over a stand-in addon (validation and error
 conventions of src/backend.js:6-56, argument packing, buffer bookkeeping,
-resident layout, kernel offsets). GPU: tests/js/host_gpu.test.js runs the MoE
+resident layout, kernel offsets) and tests/js/engine_cpu.test.js (the
+session: plan.js / interpreter.js / engine.js launch structure and rules). GPU: tests/js/host_gpu.test.js runs the MoE
 stage fused and host-driven on seeded layers; the expected routing and
 outputs come from the CPU oracle, computed here and handed over as files."""
 import json
@@ -40,6 +41,13 @@ def run_node(script, *args, timeout=600):
 
 def test_js_host_cpu():
     out = run_node("host_cpu.test.js", timeout=120)
+    assert "FAIL" not in out
+
+
+def test_js_engine_cpu():
+    # The session over the stand-in addon: program shape gate, one-token vs
+    # batch launches, chunk bookkeeping, session rules and checkpoints.
+    out = run_node("engine_cpu.test.js", timeout=120)
     assert "FAIL" not in out
 
 
