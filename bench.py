@@ -431,10 +431,10 @@ def _gemm_label(name):
     if m:
         return "k_moe_gemm_stream<%s, %d x %d tile, K/64 = %s>" % (
             "gate_up" if m.group(1) == "1" else "down", 32 * int(m.group(2)), 128 * int(m.group(3)), m.group(4))
-    m = re.search(r"k_moe_gemm_stream16ILb(\d)ELi(\d+)E", name)
+    m = re.search(r"k_moe_gemm_(stream16|rows16)ILb(\d)ELi(\d+)E", name)
     if m:
-        return "k_moe_gemm_stream16<%s, 16 x 256 tile, K/64 = %s>" % ("gate_up" if m.group(1) == "1" else "down",
-                                                                     m.group(2))
+        return "k_moe_gemm_%s<%s, 16 x 256 tile, K/64 = %s>" % (m.group(1), "gate_up" if m.group(2) == "1" else "down",
+                                                               m.group(3))
     m = re.search(r"k_split_hilo", name)
     if m:
         return "k_split_hilo"
@@ -473,7 +473,7 @@ def summarize_mfma(path, case, dest):
         mf = sum(d.get("SQ_INSTS_MFMA", 0) for d in ds) / n
         busy = sum(d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) for d in ds) / n
         va = sum(d.get("SQ_INSTS_VALU", 0) for d in ds) / n
-        rate = mf * (MFMA_FLOP_16 if "stream16" in name else MFMA_FLOP_32) / (us * 1e-6) / 1e12 if us else 0.0
+        rate = mf * (MFMA_FLOP_16 if "16<" in name else MFMA_FLOP_32) / (us * 1e-6) / 1e12 if us else 0.0
         lines.append("| %s | %d | %.1f | %.0f | %.1f | %.3f | %.3f | %.0f |" % (
             name, n, us, mf, rate, rate * 1e12 / PEAK_MFMA_F16, busy / (SIMDS * us * 1e-6 * 2.4e9) if us else 0.0,
             va))

@@ -695,6 +695,176 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
         }
 }
 
+// The 16-row kernel for K a multiple of 256, in supersteps of four scale
+// groups. Weight codes go from HBM straight to the lanes that use them: in
+// superstep S, lane (col, kq) of wave w loads the 16 code bytes of group
+// 4S + kq of weight rows n0 + 64w + 16nt + col (nt = 0..3). One load
+// instruction then reads 64 contiguous bytes of each of 16 rows (reading 16
+// bytes of each of 64 rows instead, with the weights staged through LDS,
+// streams at about half the rate), and the lane holds exactly its B operands
+// of the superstep's eight 32-wide MFMA steps: step t takes word t / 2, byte
+// half t % 2 of its group. The four lane quarters of one MFMA thus work on
+// four different groups, with the activations read to match; the sum over K
+// is the same. Activations (16 rows x 4 groups, hi/lo, 16 KiB a superstep)
+// are staged in LDS by DMA, three slots deep: lane (row col, kq) reads part t
+// of group 4S + kq. One barrier per superstep.
+__shared__ __attribute__((aligned(16))) v4u g_rows16_0[4 * 256], g_rows16_1[4 * 256], g_rows16_2[4 * 256];
+
+// An empty volatile statement that reads and rewrites the registers: code
+// using them cannot move above the volatile wait before it.
+template <int NT>
+__device__ __forceinline__ void pin_operands(v4u (&b)[NT], uint32_t (&s)[NT]) {
+#pragma unroll
+    for (int i = 0; i < NT; i++) asm volatile("" : "+v"(b[i]), "+v"(s[i]));
+}
+
+template <bool GATE_UP, int KG>
+__global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__restrict__ A, const int *__restrict__ rows,
+                                                         const int4 *__restrict__ info, const int *__restrict__ tiles,
+                                                         const uint8_t *__restrict__ arena, uint64_t stride,
+                                                         const uint8_t *__restrict__ shared_blob, int experts,
+                                                         uint64_t codes_off, uint64_t scales_off, int K, int N,
+                                                         void *__restrict__ out, int out_ld) {
+    constexpr int BN = 256, NT = 4, G = KG, NSS = KG / 4;
+    static_assert(KG % 4 == 0 && KG >= 8 && KG <= STREAM_MAX_G, "whole supersteps of four groups");
+    (void)K;
+    (void)N;
+    const int tau = blockIdx.y;
+    if (tau >= tiles[experts + 1]) return;
+    const int4 ti = info[tau];
+    const int e = ti.x, m0 = ti.y, mend = ti.z;
+    const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * BN, col = lane & 15, kq = lane >> 4;
+
+    // Activation DMA: chunk tid of a group is hi/lo tid / 128, row
+    // (tid / 8) % 16, slot tid % 8 holding part slot ^ ((row / 2) & 7).
+    const _Float16 *asrc;
+    {
+        const int hl = tid >> 7, r = (tid >> 3) & 15, part = (tid & 7) ^ ((r >> 1) & 7);
+        const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
+        const int64_t arow = GATE_UP ? rows[pos] : pos;
+        asrc = A + (arow * G * 2 + hl) * 64 + part * 8;
+    }
+    // Group j of superstep S goes to 256 j of the superstep's half.
+    auto issue_a = [&](v4u *half, int S) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) dma16(asrc + (int64_t)(4 * S + j) * 128, &half[256 * j + 64 * wave]);
+    };
+    // Byte offsets from the block's blob (32 bits: a blob is under 4 GiB),
+    // so the loads take the blob address from scalar registers.
+    const uint8_t *bcodes = blob + codes_off, *bscales = blob + scales_off;
+    uint32_t boff[NT], soff[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const uint32_t n = (uint32_t)(n0 + wave * 64 + nt * 16 + col);
+        boff[nt] = n * (G * 16) + kq * 16;
+        soff[nt] = n * (G * 2) + kq * 2;
+    }
+    auto load_b = [&](v4u (&b)[NT], int S) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) b[nt] = *(const v4u *)(bcodes + boff[nt] + S * 64);
+    };
+    auto load_s = [&](uint32_t (&s)[NT], int S) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) s[nt] = *(const uint16_t *)(bscales + soff[nt] + S * 8);
+    };
+
+    const PairMagic magic = pair_magic();
+    float4v acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) acc[nt] = (float4v){0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](const v4u *half, const v4u (&b)[NT], const uint32_t (&s)[NT]) {
+        half2v scale[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const _Float16 sh = __builtin_bit_cast(_Float16, (uint16_t)s[nt]);
+            scale[nt] = (half2v){sh, sh};
+        }
+        const v4u *ag = half + 256 * kq;  // the lane's group of the superstep
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int slot = t ^ ((col >> 1) & 7);
+            const half8 ahi = __builtin_bit_cast(half8, ag[col * 8 + slot]);
+            const half8 alo = __builtin_bit_cast(half8, ag[(16 + col) * 8 + slot]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint32_t w = (t >> 1) == 0 ? b[nt].x : (t >> 1) == 1 ? b[nt].y : (t >> 1) == 2 ? b[nt].z : b[nt].w;
+                const half8 bb = b_operand_word(w >> (8 * (t & 1)), magic, scale[nt]);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bb, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bb, acc[nt], 0, 0, 0);
+            }
+        }
+    };
+    // Superstep S in flight: 4 DMAs, 4 code loads, 4 scale loads per thread,
+    // issued in that order, all of S before any of S + 1 (memory fences
+    // between the supersteps: the waits count loads in issue order). Three
+    // slots: superstep S + 2 is issued into the slot of S - 1 once every
+    // wave has passed the barrier that starts S.
+    constexpr int PER_SS = 12;
+    v4u b0[NT], b1[NT], b2[NT];
+    uint32_t s0[NT], s1[NT], s2[NT];
+    auto issue = [&](int S) {
+        if (S % 3 == 0) {
+            issue_a(g_rows16_0, S);
+            load_b(b0, S);
+            load_s(s0, S);
+        } else if (S % 3 == 1) {
+            issue_a(g_rows16_1, S);
+            load_b(b1, S);
+            load_s(s1, S);
+        } else {
+            issue_a(g_rows16_2, S);
+            load_b(b2, S);
+            load_s(s2, S);
+        }
+        asm volatile("" ::: "memory");
+    };
+    issue(0);
+    if (NSS > 1) issue(1);
+#pragma clang loop unroll(full)
+    for (int S = 0; S < NSS; S++) {
+        // Superstep S complete for this wave (S + 1 may stay in flight),
+        // then for every wave.
+        if (S + 1 < NSS) ring_sync<PER_SS>();
+        else ring_sync<0>();
+        if (S + 2 < NSS) issue(S + 2);
+        // The unpacking of the superstep's codes stays behind the wait (the
+        // compiler would otherwise start it early and wait for every load).
+        if (S % 3 == 0) {
+            pin_operands(b0, s0);
+            compute(g_rows16_0, b0, s0);
+        } else if (S % 3 == 1) {
+            pin_operands(b1, s1);
+            compute(g_rows16_1, b1, s1);
+        } else {
+            pin_operands(b2, s2);
+            compute(g_rows16_2, b2, s2);
+        }
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int pos = m0 + 4 * kq + i, n = n0 + wave * 64 + nt * 16 + col;
+            if (GATE_UP) {
+                const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[nt][i], acc[nt][i]);
+                if ((col & 1) == 0 && pos < mend) {
+                    const float h = silu_fast(acc[nt][i]) * other;
+                    const int jj = n >> 1;
+                    _Float16 *dst =
+                        (_Float16 *)out + ((int64_t)pos * (out_ld / 64) + (jj >> 6)) * 128 + k_position(jj & 63);
+                    const _Float16 hi = (_Float16)h;
+                    dst[0] = hi;
+                    dst[64] = (_Float16)(h - (float)hi);
+                }
+            } else if (pos < mend) {
+                ((float *)out)[(int64_t)pos * out_ld + n] = acc[nt][i];
+            }
+        }
+}
+
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
 // in the reference order (kernels/strata.cu:470-476); with `resid`,
 // Y = resid + that (strata_elementwise mode 5). One block per token:
@@ -863,11 +1033,13 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                                   k_moe_gemm_stream<true, 2, 2, 32>, k_moe_gemm_stream<true, 2, 2, 40>};
             const KT big_dn[4] = {k_moe_gemm_stream<false, 2, 2, 8>, k_moe_gemm_stream<false, 2, 2, 10>,
                                   k_moe_gemm_stream<false, 2, 2, 32>, k_moe_gemm_stream<false, 2, 2, 40>};
-            using KS = decltype(&k_moe_gemm_stream16<true, 8>);
-            const KS small_gu[4] = {k_moe_gemm_stream16<true, 8>, k_moe_gemm_stream16<true, 10>,
-                                    k_moe_gemm_stream16<true, 32>, k_moe_gemm_stream16<true, 40>};
-            const KS small_dn[4] = {k_moe_gemm_stream16<false, 8>, k_moe_gemm_stream16<false, 10>,
-                                    k_moe_gemm_stream16<false, 32>, k_moe_gemm_stream16<false, 40>};
+            // 16-row tiles: whole supersteps of four groups where K allows
+            // (512, 2048, 2560), else one group per ring step (640).
+            using KS = decltype(&k_moe_gemm_rows16<true, 8>);
+            const KS small_gu[4] = {k_moe_gemm_rows16<true, 8>, k_moe_gemm_stream16<true, 10>,
+                                    k_moe_gemm_rows16<true, 32>, k_moe_gemm_rows16<true, 40>};
+            const KS small_dn[4] = {k_moe_gemm_rows16<false, 8>, k_moe_gemm_stream16<false, 10>,
+                                    k_moe_gemm_rows16<false, 32>, k_moe_gemm_rows16<false, 40>};
             const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
             const KT kb = gate_up ? big_gu[kv] : big_dn[kv];
             // The two tilings cover disjoint rows: the big-tile grid (few,
