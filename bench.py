@@ -401,7 +401,7 @@ for _case in ("512", "2048zipf"):
 MFMA_FLOP_32 = 2 * 32 * 32 * 16
 MFMA_FLOP_16 = 2 * 16 * 16 * 32
 SIMDS = 256 * 4
-DECODE_KERNELS = ["k_decode_route", "k_decode_gate_up", "k_decode_down"]
+DECODE_KERNELS = ["k_decode_fused", "k_decode_route", "k_decode_gate_up", "k_decode_down"]
 
 
 def _csv_rows(path):
@@ -508,9 +508,10 @@ def summarize(out_dir):
     f_fac, w_fac = copy_bytes / (cal_f * 1024), copy_bytes / (cal_w * 1024)
     W, F, E, K = 2048, 512, 512, 10
     algo = decode_kernel_bytes(W, F, E, K)
-    algo_by_kernel = {"k_decode_route": algo["decode_route"], "k_decode_gate_up": algo["decode_gate_up"],
-                      "k_decode_down": algo["decode_down_combine"]}
-    traffic, md = {}, ["# HBM traffic per launch: decode T=1 kernels (8 rotated layers)", "",
+    algo_by_kernel = {"k_decode_fused": sum(algo.values()), "k_decode_route": algo["decode_route"],
+                      "k_decode_gate_up": algo["decode_gate_up"], "k_decode_down": algo["decode_down_combine"]}
+    traffic, md = {}, ["# HBM traffic per launch: decode T=1 kernels (8 rotated layers: the single-launch "
+                       "layer k_decode_fused and the three-kernel path; L2-miss bytes, durations not used)", "",
                        "Commands (from the repository root):", ""]
     md += ["    " + PROFILE_CMDS[k] for k in ("fetch", "write", "cal_fetch", "cal_write")]
     md += ["", "Calibration: the copy kernel (strata_elementwise, 256 MiB read + 256 MiB written per launch) "
