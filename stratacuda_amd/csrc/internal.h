@@ -17,6 +17,9 @@ struct sm_ctx {
     // forked from and joined back to `stream` with the two events.
     hipStream_t aux = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    // Marks a point on `aux` that `stream` can wait for without waiting for
+    // the rest of the aux work (aux_mark / wait_aux_mark).
+    hipEvent_t mid = nullptr;
     std::map<uint64_t, uint64_t> buffers;  // handle (device address) -> bytes
     std::string error;
     hipEvent_t events[64] = {};
@@ -64,6 +67,11 @@ int launched(sm_ctx *ctx);  // checks hipGetLastError after a launch
 // after everything queued on ctx->aux so far. Both are graph-capturable.
 int fork_aux(sm_ctx *ctx);
 int join_aux(sm_ctx *ctx);
+// aux_mark: records the work queued on ctx->aux so far; wait_aux_mark: work
+// queued on ctx->stream after this runs after that work (not after aux work
+// queued later).
+int aux_mark(sm_ctx *ctx);
+int wait_aux_mark(sm_ctx *ctx);
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

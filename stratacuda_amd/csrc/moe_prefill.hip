@@ -30,10 +30,12 @@
 //  * Tiles (width and ff among 512 / 2048, the benchmark shapes): segments of
 //    more than 32 rows run in 64 x 256 blocks on v_mfma_f32_32x32x16_f16
 //    (k_moe_gemm_stream), shorter ones in 16 x 256 blocks on
-//    v_mfma_f32_16x16x32_f16 (k_moe_gemm_stream16); the two grids cover
-//    disjoint rows and run on two streams. Both stream A and B through a ring
-//    of LDS stages filled by direct global->LDS loads. Each block reads its
-//    tile record (segment, first row, end row) written by the dispatch.
+//    v_mfma_f32_16x16x32_f16 (k_moe_gemm_rows16, k_moe_gemm_stream16); the
+//    two grids cover disjoint rows and run on two streams. Each block reads
+//    its tile record (segment, first row, end row, segment start) written by
+//    the dispatch, or for the shared expert's segment by k_shared_tiles: the
+//    shared expert needs no routing, so its GEMMs run on the second stream
+//    from the start, beside the router and the dispatch.
 //    Other shapes use k_moe_gemm (register-held B, A double-buffered in LDS,
 //    64- and 32-row tiles).
 //    grid.x = n-block (fastest) so the m-tiles of one (expert, n-block) run
@@ -457,7 +459,9 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     for (int i = 0; i < ACH; i++) {
         const int c = tid + 256 * i, hl = c / (8 * BM), r = (c >> 3) % BM, part = (c & 7) ^ ((r >> 1) & 7);
         const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
-        const int64_t arow = GATE_UP ? rows[pos] : pos;
+        // gate/up: the routed rows' tokens from the dispatch; the shared
+        // expert's segment holds every token in order from its start
+        const int64_t arow = GATE_UP ? (e < experts ? rows[pos] : pos - ti.w) : pos;
         asrc[i] = A + (arow * G * 2 + hl) * 64 + part * 8;
     }
     const uint8_t *bsrc[BCH];
@@ -609,7 +613,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
     {
         const int hl = tid >> 7, r = (tid >> 3) & 15, part = (tid & 7) ^ ((r >> 1) & 7);
         const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
-        const int64_t arow = GATE_UP ? rows[pos] : pos;
+        const int64_t arow = GATE_UP ? (e < experts ? rows[pos] : pos - ti.w) : pos;
         asrc = A + (arow * G * 2 + hl) * 64 + part * 8;
     }
     const uint8_t *bsrc = blob + codes_off + (uint64_t)(n0 + tid) * (G * 16);
@@ -743,7 +747,7 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
     {
         const int hl = tid >> 7, r = (tid >> 3) & 15, part = (tid & 7) ^ ((r >> 1) & 7);
         const int pos = min(m0 + r, mend - 1);  // rows past the end load the segment's last row
-        const int64_t arow = GATE_UP ? rows[pos] : pos;
+        const int64_t arow = GATE_UP ? (e < experts ? rows[pos] : pos - ti.w) : pos;
         asrc = A + (arow * G * 2 + hl) * 64 + part * 8;
     }
     // Group j of superstep S goes to 256 j of the superstep's half.
@@ -865,6 +869,17 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
         }
 }
 
+// Tile records of the shared expert's segment, rows [first, first + rows)
+// (every token in order), in tiles of mt rows: tiles[experts + 1] = count and
+// record j = (experts, first + j mt, first + rows, first), the layout the
+// dispatch writes for the routed segments.
+__global__ void k_shared_tiles(int4 *__restrict__ info, int *__restrict__ tiles, int experts, int first, int rows,
+                               int mt) {
+    const int n = (rows + mt - 1) / mt;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) info[j] = make_int4(experts, first + j * mt, first + rows, first);
+    if (threadIdx.x == 0) tiles[experts + 1] = n;
+}
+
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
 // in the reference order (kernels/strata.cu:470-476); with `resid`,
 // Y = resid + that (strata_elementwise mode 5). One block per token:
@@ -874,8 +889,8 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
 constexpr int COMBINE_MAX_K = 32;
 __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, const int *__restrict__ where_,
                                                  const float *__restrict__ weights, const float *__restrict__ gate,
-                                                 const int *__restrict__ offsets, float *__restrict__ Y, int tokens,
-                                                 int topk, int width, int experts, const float *__restrict__ resid) {
+                                                 int64_t shared_base, float *__restrict__ Y, int tokens,
+                                                 int topk, int width, const float *__restrict__ resid) {
     __shared__ int s_pos[COMBINE_MAX_K];
     __shared__ float s_w[COMBINE_MAX_K];
     __shared__ float s_sig;
@@ -887,7 +902,7 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, co
     if (tid == 0) s_sig = sm::sigmoid(gate[t]);
     __syncthreads();
     const float sig = s_sig;
-    const float4 *shared_row = (const float4 *)(P + ((int64_t)offsets[experts] + t) * width);
+    const float4 *shared_row = (const float4 *)(P + (shared_base + t) * width);
     for (int d4 = tid; d4 < width / 4; d4 += blockDim.x) {
         const float4 s = shared_row[d4];
         float4 v = {s.x * sig, s.y * sig, s.z * sig, s.w * sig};
@@ -916,6 +931,8 @@ inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // rows) in 16-row tiles, so the 64-row grid is not launched; larger ones
 // tile segments of more than 32 rows in 64-row tiles.
 constexpr int kSmallBatch = 64;
+// Largest batch whose shared-expert products run beside the router.
+constexpr int kSharedFirstMaxTokens = 1024;
 inline int tiling_split(int tokens) { return tokens <= kSmallBatch ? kSmallBatch + 1 : 33; }
 
 // Grid bounds of the two tilings over the experts + 1 segments of m rows:
@@ -932,8 +949,8 @@ inline uint64_t big_tile_bound(uint64_t m, int experts) {
 }
 
 struct PrefillWs {
-    uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, rows, parts, where_, Xhl,
-        Hhl, P, Xn, end;
+    uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, tiles_shared, info_shared,
+        rows, parts, where_, Xhl, Hhl, P, Xn, end;
 };
 PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool block = false) {
     const uint64_t n = (uint64_t)tokens * topk, m = n + tokens;
@@ -946,7 +963,9 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool 
     w.tiles_big = up(w.tiles_small + ((uint64_t)experts + 2) * 4);
     w.info_small = up(w.tiles_big + ((uint64_t)experts + 2) * 4);
     w.info_big = up(w.info_small + small_tile_bound(m, experts, tiling_split(tokens)) * 16);
-    w.rows = up(w.info_big + big_tile_bound(m, experts) * 16);
+    w.tiles_shared = up(w.info_big + big_tile_bound(m, experts) * 16);
+    w.info_shared = up(w.tiles_shared + ((uint64_t)experts + 2) * 4);
+    w.rows = up(w.info_shared + ((uint64_t)tokens / 16 + 1) * 16);
     w.parts = up(w.rows + m * 4);
     w.where_ = up(w.parts + m * 4);
     w.Xhl = up(w.where_ + n * 4);
@@ -983,38 +1002,100 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     BlobLayout L = blob_layout(width, ff);
     if ((2 * ff) % 128 || width % 128)
         return fail(ctx, SM_E_ARG, "prefill needs width and 2*ff to be multiples of 128");
-    if (int rc = stage_mark(ctx, kStagePrefillRoute)) return rc;
-    if (int rc = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts,
-                              topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
-                              (float *)(ws + w.gate)))
-        return rc;
-    if (int rc = stage_mark(ctx, kStagePrefillDispatch)) return rc;
-    // The hi/lo split of the activations needs only X: it runs on the second
-    // stream beside the dispatch kernels, which occupy few CUs.
-    if (int rc = fork_aux(ctx)) return rc;
-    const int64_t groups = (int64_t)tokens * (width / 64);
-    k_split_hilo<<<(unsigned)((groups * 8 + 255) / 256), 256, 0, ctx->aux>>>((const float *)X,
-                                                                            (_Float16 *)(ws + w.Xhl), groups);
-    int *offsets = (int *)(ws + w.offsets);
-    int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);
     // Streaming kernels: N a multiple of 256 and K one of the compiled group
     // counts in both products (512, 640, 2048, 2560: the benchmark's and the
     // real model's shapes). Segments of up to 32 rows then run in 16-row
     // tiles, else in one 32-row tile; longer ones in 64-row tiles.
     auto streamable = [](int k) { return k == 512 || k == 640 || k == 2048 || k == 2560; };
     const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && streamable(width) && streamable(ff);
-    const int4 *info_small = (const int4 *)(ws + w.info_small), *info_big = (const int4 *)(ws + w.info_big);
     const int split = stream ? tiling_split(tokens) : 33;
+    const int64_t routed_rows = (int64_t)tokens * topk;  // the shared expert's segment starts here
+    const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
+    const uint8_t *ar = (const uint8_t *)arena, *sh = (const uint8_t *)shared_blob;
+
+    // Streaming GEMM launchers by K: 64-row tiles, and 16-row tiles in whole
+    // supersteps of four groups where K allows (512, 2048, 2560), else one
+    // group per ring step (640).
+    using KT = decltype(&k_moe_gemm_stream<true, 2, 2, 8>);
+    auto big_kernel = [](bool gate_up, int K) -> KT {
+        const KT gu[4] = {k_moe_gemm_stream<true, 2, 2, 8>, k_moe_gemm_stream<true, 2, 2, 10>,
+                          k_moe_gemm_stream<true, 2, 2, 32>, k_moe_gemm_stream<true, 2, 2, 40>};
+        const KT dn[4] = {k_moe_gemm_stream<false, 2, 2, 8>, k_moe_gemm_stream<false, 2, 2, 10>,
+                          k_moe_gemm_stream<false, 2, 2, 32>, k_moe_gemm_stream<false, 2, 2, 40>};
+        const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
+        return gate_up ? gu[kv] : dn[kv];
+    };
+    auto small_kernel = [](bool gate_up, int K) -> KT {
+        const KT gu[4] = {k_moe_gemm_rows16<true, 8>, k_moe_gemm_stream16<true, 10>, k_moe_gemm_rows16<true, 32>,
+                          k_moe_gemm_rows16<true, 40>};
+        const KT dn[4] = {k_moe_gemm_rows16<false, 8>, k_moe_gemm_stream16<false, 10>, k_moe_gemm_rows16<false, 32>,
+                          k_moe_gemm_rows16<false, 40>};
+        const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
+        return gate_up ? gu[kv] : dn[kv];
+    };
+
+    // Second stream, from the start: X's hi/lo split, then (streaming shapes,
+    // up to kSharedFirstMaxTokens tokens) the shared expert's gate/up and down
+    // products over every token, which need no routing; they run beside the
+    // router and the dispatch. At larger T the router's VALU work fills the
+    // GPU and the shared products only slow it down (T=2048: layer 2 % slower
+    // in an A/B on one GPU; T=512: 1-2.5 % faster), so the dispatch tiles the
+    // shared segment with the routed ones there.
+    const bool shared_first = stream && tokens <= kSharedFirstMaxTokens;
+    if (int rc = fork_aux(ctx)) return rc;
+    const int64_t groups = (int64_t)tokens * (width / 64);
+    k_split_hilo<<<(unsigned)((groups * 8 + 255) / 256), 256, 0, ctx->aux>>>((const float *)X,
+                                                                            (_Float16 *)(ws + w.Xhl), groups);
+    int rc = launched(ctx);
+    if (rc == SM_OK) rc = aux_mark(ctx);  // the hi/lo activations are ready here
+    if (rc == SM_OK && shared_first) {
+        // The shared segment in 64-row tiles when it is long enough for them
+        // (the routed segments' rule), else in 16-row tiles.
+        const bool big = tokens >= split;
+        const int mt = big ? 64 : 16, ntiles = (tokens + mt - 1) / mt;
+        int4 *info_sh = (int4 *)(ws + w.info_shared);
+        int *tiles_sh = (int *)(ws + w.tiles_shared);
+        k_shared_tiles<<<1, 256, 0, ctx->aux>>>(info_sh, tiles_sh, experts, (int)routed_rows, tokens, mt);
+        rc = launched(ctx);
+        if (rc == SM_OK) {
+            const KT k = big ? big_kernel(true, width) : small_kernel(true, width);
+            k<<<dim3((unsigned)(2 * ff / 256), (unsigned)ntiles), 256, 0, ctx->aux>>>(
+                xhl, (const int *)(ws + w.rows), info_sh, tiles_sh, ar, blob_stride, sh, experts, L.gate_up_codes, L.gate_up_scales,
+                width, 2 * ff, ws + w.Hhl, ff);
+            rc = launched(ctx);
+        }
+        if (rc == SM_OK) {
+            const KT k = big ? big_kernel(false, ff) : small_kernel(false, ff);
+            k<<<dim3((unsigned)(width / 256), (unsigned)ntiles), 256, 0, ctx->aux>>>(
+                hhl, nullptr, info_sh, tiles_sh, ar, blob_stride, sh, experts, L.down_codes, L.down_scales, ff, width,
+                ws + w.P, width);
+            rc = launched(ctx);
+        }
+    }
+    if (rc) {
+        (void)join_aux(ctx);
+        return rc;
+    }
+
+    if (int rc2 = stage_mark(ctx, kStagePrefillRoute)) return rc2;
+    if (int rc2 = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts,
+                               topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
+                               (float *)(ws + w.gate)))
+        return rc2;
+    if (int rc2 = stage_mark(ctx, kStagePrefillDispatch)) return rc2;
+    int *offsets = (int *)(ws + w.offsets);
+    int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);
+    const int4 *info_small = (const int4 *)(ws + w.info_small), *info_big = (const int4 *)(ws + w.info_big);
     GemmTiling tiling = {tiles_small, tiles_big, split, stream ? 16 : 32, 64};
     tiling.info_small = (int *)info_small;
     tiling.info_big = (int *)info_big;
-    int rc = launched(ctx);
-    if (rc == SM_OK)
-        rc = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
-                             (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, &tiling);
-    const int rc_join = join_aux(ctx);
-    if (rc) return rc;
-    if (rc_join) return rc_join;
+    // The dispatch tiles the shared expert's segment only where it is not
+    // computed on the second stream already.
+    if (int rc2 = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
+                                  (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch,
+                                  shared_first ? 0 : 1, &tiling))
+        return rc2;
+    if (int rc2 = wait_aux_mark(ctx)) return rc2;
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const uint64_t segs = (uint64_t)experts + 1;
     // Segment tilings: `split` or more rows in 64-row tiles ("big"), fewer in
@@ -1022,40 +1103,23 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     const unsigned big_tiles = (unsigned)big_tile_bound(m, experts);
     const unsigned small_tiles = (unsigned)(stream ? small_tile_bound(m, experts, split) : segs + 1);
     const bool any_big = split <= 33;  // otherwise no segment reaches the big tiling
-    const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
     const int *rows = (const int *)(ws + w.rows);
-    const uint8_t *ar = (const uint8_t *)arena, *sh = (const uint8_t *)shared_blob;
     auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
                      void *out, int ld) -> int {
         if (stream) {
-            using KT = decltype(&k_moe_gemm_stream<true, 2, 2, 8>);
-            const KT big_gu[4] = {k_moe_gemm_stream<true, 2, 2, 8>, k_moe_gemm_stream<true, 2, 2, 10>,
-                                  k_moe_gemm_stream<true, 2, 2, 32>, k_moe_gemm_stream<true, 2, 2, 40>};
-            const KT big_dn[4] = {k_moe_gemm_stream<false, 2, 2, 8>, k_moe_gemm_stream<false, 2, 2, 10>,
-                                  k_moe_gemm_stream<false, 2, 2, 32>, k_moe_gemm_stream<false, 2, 2, 40>};
-            // 16-row tiles: whole supersteps of four groups where K allows
-            // (512, 2048, 2560), else one group per ring step (640).
-            using KS = decltype(&k_moe_gemm_rows16<true, 8>);
-            const KS small_gu[4] = {k_moe_gemm_rows16<true, 8>, k_moe_gemm_stream16<true, 10>,
-                                    k_moe_gemm_rows16<true, 32>, k_moe_gemm_rows16<true, 40>};
-            const KS small_dn[4] = {k_moe_gemm_rows16<false, 8>, k_moe_gemm_stream16<false, 10>,
-                                    k_moe_gemm_rows16<false, 32>, k_moe_gemm_rows16<false, 40>};
-            const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
-            const KT kb = gate_up ? big_gu[kv] : big_dn[kv];
             // The two tilings cover disjoint rows: the big-tile grid (few,
             // long blocks at small T) runs on the second stream beside the
-            // small-tile grid.
+            // small-tile grid (after the shared expert's products there).
             int rc_big = SM_OK;
             if (any_big) {
-                if (int rc = fork_aux(ctx)) return rc;
-                kb<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(
+                if (int rc3 = fork_aux(ctx)) return rc3;
+                big_kernel(gate_up, K)<<<dim3((unsigned)(N / 256), big_tiles), 256, 0, ctx->aux>>>(
                     a, r, info_big, tiles_big, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
                 rc_big = launched(ctx);
             }
-            const KS ks = gate_up ? small_gu[kv] : small_dn[kv];
             int rc_small = SM_OK;
             if (rc_big == SM_OK) {
-                ks<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
+                small_kernel(gate_up, K)<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
                     a, r, info_small, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
                 rc_small = launched(ctx);
             }
@@ -1071,7 +1135,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
             kb<<<dim3((unsigned)(N / 128), big_tiles), 256, 0, ctx->stream>>>(a, r, info_big, tiles_big, ar, blob_stride,
                                                                              sh, experts, codes, scales, K, N, out, ld);
         }
-        if (int rc = launched(ctx)) return rc;
+        if (int rc3 = launched(ctx)) return rc3;
         if (N % 1024 == 0) {
             auto ks = gate_up ? k_moe_gemm<true, 1, 4, 1, 8> : k_moe_gemm<false, 1, 4, 1, 8>;
             ks<<<dim3((unsigned)(N / 1024), small_tiles), 512, 0, ctx->stream>>>(
@@ -1083,16 +1147,17 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         }
         return launched(ctx);
     };
-    if (int rc = stage_mark(ctx, kStagePrefillGateUp)) return rc;
-    if (int rc = gemms(true, xhl, rows, width, 2 * ff, L.gate_up_codes, L.gate_up_scales, ws + w.Hhl, ff)) return rc;
-    if (int rc = stage_mark(ctx, kStagePrefillDown)) return rc;
-    if (int rc = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return rc;
-    const uint64_t total = (uint64_t)tokens * width;
-    if (int rc = stage_mark(ctx, kStagePrefillCombine)) return rc;
-    (void)total;
+    if (int rc2 = stage_mark(ctx, kStagePrefillGateUp)) return rc2;
+    if (int rc2 = gemms(true, xhl, rows, width, 2 * ff, L.gate_up_codes, L.gate_up_scales, ws + w.Hhl, ff)) return rc2;
+    if (int rc2 = stage_mark(ctx, kStagePrefillDown)) return rc2;
+    if (int rc2 = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return rc2;
+    // Everything on the second stream (the shared expert's products) is in
+    // before the combine reads P.
+    if (int rc2 = join_aux(ctx)) return rc2;
+    if (int rc2 = stage_mark(ctx, kStagePrefillCombine)) return rc2;
     k_combine<<<(unsigned)tokens, 256, 0, ctx->stream>>>(
         (const float *)(ws + w.P), (const int *)(ws + w.where_), (const float *)weights, (const float *)(ws + w.gate),
-        offsets, (float *)Y, tokens, topk, width, experts, resid);
+        routed_rows, (float *)Y, tokens, topk, width, resid);
     if (int rc = launched(ctx)) return rc;
     return stage_mark(ctx, -1);
 }

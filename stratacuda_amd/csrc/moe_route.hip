@@ -303,7 +303,7 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_scan(const int *__res
         int4 *info = ns ? info_small : info_big;
         const int n = ns ? ns : nbg, mt = ns ? mt_small : mt_big, first = (ns ? ts : tb) - n;
         if (info)
-            for (int j = 0; j < n; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, 0);
+            for (int j = 0; j < n; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, excl);
     }
     if (e <= experts) {
         if (tile_small) tile_small[e + 1] = ts;
@@ -370,7 +370,7 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_one(const int *__rest
         int4 *info = ns ? info_small : info_big;
         const int cnt_t = ns ? ns : nbg, mt = ns ? mt_small : mt_big, first = (ns ? ts : tb) - cnt_t;
         if (info)
-            for (int j = 0; j < cnt_t; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, 0);
+            for (int j = 0; j < cnt_t; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, excl);
     }
     __syncthreads();  // s_off complete
     for (int a = tid; a < n + (extra ? tokens : 0); a += SCAN_THREADS) {

@@ -49,6 +49,16 @@ int join_aux(sm_ctx *ctx) {
     return err == hipSuccess ? SM_OK : hip_fail(ctx, err, "stream join");
 }
 
+int aux_mark(sm_ctx *ctx) {
+    const hipError_t err = hipEventRecord(ctx->mid, ctx->aux);
+    return err == hipSuccess ? SM_OK : hip_fail(ctx, err, "aux mark");
+}
+
+int wait_aux_mark(sm_ctx *ctx) {
+    const hipError_t err = hipStreamWaitEvent(ctx->stream, ctx->mid, 0);
+    return err == hipSuccess ? SM_OK : hip_fail(ctx, err, "wait for aux mark");
+}
+
 // Folds recorded stage events into the per-stage totals (synchronises).
 static int stage_fold(sm_ctx *ctx) {
     if (ctx->marks.empty()) return SM_OK;
@@ -108,7 +118,8 @@ int sm_init(int device, sm_ctx **out) {
     }
     if (hipStreamCreateWithFlags(&ctx->aux, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->mid, hipEventDisableTiming) != hipSuccess) {
         sm_shutdown(ctx);
         return SM_E_HIP;
     }
@@ -148,6 +159,7 @@ void sm_shutdown(sm_ctx *ctx) {
         if (e) (void)hipEventDestroy(e);
     if (ctx->fork) (void)hipEventDestroy(ctx->fork);
     if (ctx->join) (void)hipEventDestroy(ctx->join);
+    if (ctx->mid) (void)hipEventDestroy(ctx->mid);
     if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
