@@ -345,6 +345,17 @@ __device__ __forceinline__ void ring_sync() {
     asm volatile("" ::: "memory");
 }
 
+// This block's tile and column block. The hardware hands block L (x
+// fastest) to XCD L % 8; block L takes tile (L / 8 / nx) * 8 + L % 8 and
+// column block (L / 8) % nx, so all column blocks of one tile run on one XCD
+// and read the tile's activation rows through one L2. Needs gridDim.y a
+// multiple of 8 (the host rounds the tile bound up).
+__device__ __forceinline__ void xcd_tile(int &tau, int &cb) {
+    const int nx = gridDim.x, L = blockIdx.y * nx + blockIdx.x, idx = L >> 3;
+    tau = (idx / nx) * 8 + (L & 7);
+    cb = idx % nx;
+}
+
 constexpr int STREAM_MAX_G = 40;  // K <= 2560 for the streaming kernels (the real model's width)
 
 // The G fp16 scales of one weight row (2G contiguous bytes) into G/2 words:
@@ -440,7 +451,8 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     static_assert(KG >= 8 && KG <= STREAM_MAX_G && KG % 2 == 0, "K / 64 groups");
     static_assert(BM <= 64 && BN <= 256, "stage size");
     // Tile record (segment, first row, end of the segment) from the dispatch.
-    const int tau = blockIdx.y;
+    int tau, cb;
+    xcd_tile(tau, cb);
     if (tau >= tiles[experts + 1]) return;
     const int4 ti = info[tau];
     const int e = ti.x, m0 = ti.y, mend = ti.z;
@@ -448,7 +460,7 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream(const _Float16 *__restr
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     constexpr int G = KG;  // K / 64, fixed at compile time: the ring is straight-line code
     (void)K;
-    const int n0 = blockIdx.x * BN;
+    const int n0 = cb * BN;
 
     // Per-thread DMA sources. A chunk c = tid + 256 i: hi/lo c / (8 BM), row
     // (c / 8) % BM, slot c % 8 holding part slot ^ ((row / 2) & 7). A 128-bit
@@ -598,13 +610,14 @@ __global__ void __launch_bounds__(256) k_moe_gemm_stream16(const _Float16 *__res
     (void)K;
     (void)N;
     // Tile record (segment, first row, end of the segment) from the dispatch.
-    const int tau = blockIdx.y;
+    int tau, cb;
+    xcd_tile(tau, cb);
     if (tau >= tiles[experts + 1]) return;
     const int4 ti = info[tau];
     const int e = ti.x, m0 = ti.y, mend = ti.z;
     const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * BN;
+    const int n0 = cb * BN;
 
     // DMA sources, one A and one B load per thread per stage. A chunk
     // c = tid: hi/lo c / 128, row (c / 8) % 16, slot c % 8 holding part
@@ -733,13 +746,14 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
     static_assert(KG % 4 == 0 && KG >= 8 && KG <= STREAM_MAX_G, "whole supersteps of four groups");
     (void)K;
     (void)N;
-    const int tau = blockIdx.y;
+    int tau, cb;
+    xcd_tile(tau, cb);
     if (tau >= tiles[experts + 1]) return;
     const int4 ti = info[tau];
     const int e = ti.x, m0 = ti.y, mend = ti.z;
     const uint8_t *blob = e < experts ? arena + (uint64_t)e * stride : shared_blob;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * BN, col = lane & 15, kq = lane >> 4;
+    const int n0 = cb * BN, col = lane & 15, kq = lane >> 4;
 
     // Activation DMA: chunk tid of a group is hi/lo tid / 128, row
     // (tid / 8) % 16, slot tid % 8 holding part slot ^ ((row / 2) & 7).
@@ -1052,7 +1066,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         // The shared segment in 64-row tiles when it is long enough for them
         // (the routed segments' rule), else in 16-row tiles.
         const bool big = tokens >= split;
-        const int mt = big ? 64 : 16, ntiles = (tokens + mt - 1) / mt;
+        const int mt = big ? 64 : 16, ntiles = ((tokens + mt - 1) / mt + 7) / 8 * 8;  // grid: multiple of 8
         int4 *info_sh = (int4 *)(ws + w.info_shared);
         int *tiles_sh = (int *)(ws + w.tiles_shared);
         k_shared_tiles<<<1, 256, 0, ctx->aux>>>(info_sh, tiles_sh, experts, (int)routed_rows, tokens, mt);
@@ -1100,8 +1114,10 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     const uint64_t segs = (uint64_t)experts + 1;
     // Segment tilings: `split` or more rows in 64-row tiles ("big"), fewer in
     // 16-row tiles (streaming kernels) or one 32-row tile (k_moe_gemm).
-    const unsigned big_tiles = (unsigned)big_tile_bound(m, experts);
-    const unsigned small_tiles = (unsigned)(stream ? small_tile_bound(m, experts, split) : segs + 1);
+    // (the streaming kernels' grids: tile bounds rounded up to a multiple of 8, see xcd_tile)
+    auto round8 = [](uint64_t v) { return (unsigned)((v + 7) / 8 * 8); };
+    const unsigned big_tiles = stream ? round8(big_tile_bound(m, experts)) : (unsigned)big_tile_bound(m, experts);
+    const unsigned small_tiles = stream ? round8(small_tile_bound(m, experts, split)) : (unsigned)(segs + 1);
     const bool any_big = split <= 33;  // otherwise no segment reaches the big tiling
     const int *rows = (const int *)(ws + w.rows);
     auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
