@@ -84,6 +84,7 @@ def test_route_bit_exact(backend, oracle, full_layer, tokens, bias):
 
 @pytest.mark.parametrize("tokens,topk,experts,zipf", [(1, 10, 512, False), (63, 10, 512, False),
                                                       (65, 3, 16, False), (300, 4, 40, True),
+                                                      (512, 10, 512, False), (513, 10, 512, True),
                                                       (2048, 10, 512, True)])
 def test_dispatch_bit_exact(backend, oracle, tokens, topk, experts, zipf):
     rng = np.random.default_rng(tokens + experts)
