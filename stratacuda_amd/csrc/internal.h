@@ -130,7 +130,7 @@ struct BlockArgs {
 // a token dimension; larger ones the dispatch + grouped GEMM path.
 constexpr int kDecodeMaxTokens = 24;
 constexpr int kDecodeBlockRouting = 4;  // up to this many tokens the gate/up blocks route
-constexpr int kRouteRowsMaxTokens = 64;  // router logits one wave per (row, token) up to here
+constexpr int kRouteRowsMaxTokens = 8;  // router logits one wave per (row, token) up to here
 // Exact per-token top-k (strata_router order) of logits [tokens x experts].
 int topk_launch(sm_ctx *ctx, const float *logits, int *ids, float *weights, int tokens, int experts, int topk);
 int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,

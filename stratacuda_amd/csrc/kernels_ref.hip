@@ -262,6 +262,32 @@ __global__ void k_norm(const float *X, const float *W, float *Y, int cols, int r
     }
 }
 
+// The stack block's RMSNorm (k_norm mode 0, one gamma row, scale 1) for
+// rows of NJ x 64 values held in registers: every load of a lane is issued
+// before the sum (k_norm's batches of eight wait on each other), the same
+// lane-strided order and tree, so the results are bit-identical.
+template <int NJ>
+__global__ void k_norm_reg(const float *X, const float *W, float *Y, int rows, float epsilon) {
+    uint64_t g;
+    if (!logical_group((uint64_t)rows, g)) return;
+    const int row = (int)g, lane = lane_id();
+    constexpr int cols = NJ * 64;
+    const float *xr = X + (int64_t)row * cols;
+    float x[NJ], w[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) x[j] = xr[lane + 64 * j];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) w[j] = W[lane + 64 * j];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) ss = ss + x[j] * x[j];
+    ss = __shfl(sm::tree_sum64(ss), 0, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)cols + epsilon);
+    float *yr = Y + (int64_t)row * cols;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) yr[lane + 64 * j] = x[j] * inv * w[j];
+}
+
 // kernels/strata.cu:230-236 strata_elementwise
 __global__ void k_elementwise(const float *A, const float *B, float *Y, int n, int mode, float scale) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -713,8 +739,13 @@ const Entry *find_entry(const char *name) {
 namespace smi {
 
 int norm_launch(sm_ctx *ctx, const float *X, const float *gamma, float *Y, int cols, int rows, float eps) {
-    k_norm<<<blocks_for((uint64_t)rows), 256, 0, ctx->stream>>>(X, gamma, Y, cols, rows, 1, 0, eps, 1.0f,
-                                                              (uint64_t)rows);
+    if (cols == 2048)
+        k_norm_reg<32><<<blocks_for((uint64_t)rows), 256, 0, ctx->stream>>>(X, gamma, Y, rows, eps);
+    else if (cols == 2560)
+        k_norm_reg<40><<<blocks_for((uint64_t)rows), 256, 0, ctx->stream>>>(X, gamma, Y, rows, eps);
+    else
+        k_norm<<<blocks_for((uint64_t)rows), 256, 0, ctx->stream>>>(X, gamma, Y, cols, rows, 1, 0, eps, 1.0f,
+                                                                  (uint64_t)rows);
     return launched(ctx);
 }
 

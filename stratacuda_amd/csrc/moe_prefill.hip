@@ -735,15 +735,18 @@ __device__ __forceinline__ void pin_operands(v4u (&b)[NT], uint32_t (&s)[NT]) {
     for (int i = 0; i < NT; i++) asm volatile("" : "+v"(b[i]), "+v"(s[i]));
 }
 
-template <bool GATE_UP, int KG>
+template <bool GATE_UP, int KG, int NT = 4>
 __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__restrict__ A, const int *__restrict__ rows,
                                                          const int4 *__restrict__ info, const int *__restrict__ tiles,
                                                          const uint8_t *__restrict__ arena, uint64_t stride,
                                                          const uint8_t *__restrict__ shared_blob, int experts,
                                                          uint64_t codes_off, uint64_t scales_off, int K, int N,
                                                          void *__restrict__ out, int out_ld) {
-    constexpr int BN = 256, NT = 4, G = KG, NSS = KG / 4;
+    // NT column tiles of 16 per wave: a block covers 64 NT weight rows (NT = 4
+    // for most batches; 1 where few tiles would leave the GPU idle).
+    constexpr int BN = 64 * NT, G = KG, NSS = KG / 4;
     static_assert(KG % 4 == 0 && KG >= 8 && KG <= STREAM_MAX_G, "whole supersteps of four groups");
+    static_assert(NT == 1 || NT == 2 || NT == 4, "1, 2 or 4 column tiles per wave");
     (void)K;
     (void)N;
     int tau, cb;
@@ -775,7 +778,7 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
     uint32_t boff[NT], soff[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        const uint32_t n = (uint32_t)(n0 + wave * 64 + nt * 16 + col);
+        const uint32_t n = (uint32_t)(n0 + wave * 16 * NT + nt * 16 + col);
         boff[nt] = n * (G * 16) + kq * 16;
         soff[nt] = n * (G * 2) + kq * 2;
     }
@@ -814,12 +817,12 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
             }
         }
     };
-    // Superstep S in flight: 4 DMAs, 4 code loads, 4 scale loads per thread,
-    // issued in that order, all of S before any of S + 1 (memory fences
-    // between the supersteps: the waits count loads in issue order). Three
-    // slots: superstep S + 2 is issued into the slot of S - 1 once every
-    // wave has passed the barrier that starts S.
-    constexpr int PER_SS = 12;
+    // Superstep S in flight: 4 DMAs, NT code loads, NT scale loads per
+    // thread, issued in that order, all of S before any of S + 1 (memory
+    // fences between the supersteps: the waits count loads in issue order).
+    // Three slots: superstep S + 2 is issued into the slot of S - 1 once
+    // every wave has passed the barrier that starts S.
+    constexpr int PER_SS = 4 + 2 * NT;
     v4u b0[NT], b1[NT], b2[NT];
     uint32_t s0[NT], s1[NT], s2[NT];
     auto issue = [&](int S) {
@@ -865,7 +868,7 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
     for (int nt = 0; nt < NT; nt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int pos = m0 + 4 * kq + i, n = n0 + wave * 64 + nt * 16 + col;
+            const int pos = m0 + 4 * kq + i, n = n0 + wave * 16 * NT + nt * 16 + col;
             if (GATE_UP) {
                 const float other = sm::dpp_f32<sm::kDppQuadXor1>(acc[nt][i], acc[nt][i]);
                 if ((col & 1) == 0 && pos < mend) {
@@ -917,18 +920,30 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, co
     __syncthreads();
     const float sig = s_sig;
     const float4 *shared_row = (const float4 *)(P + (shared_base + t) * width);
-    for (int d4 = tid; d4 < width / 4; d4 += blockDim.x) {
+    // block (t, c) covers float4 columns c x 256 + tid, in steps of the
+    // grid's column extent
+    for (int d4 = blockIdx.y * blockDim.x + tid; d4 < width / 4; d4 += blockDim.x * gridDim.y) {
         const float4 s = shared_row[d4];
         float4 v = {s.x * sig, s.y * sig, s.z * sig, s.w * sig};
-        for (int k = 0; k < topk; k++) {
-            const int pos = s_pos[k];
-            const float w = s_w[k];
-            float4 part = {__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
-            if (pos >= 0) part = ((const float4 *)(P + (int64_t)pos * width))[d4];
-            v.x = v.x + part.x * w;
-            v.y = v.y + part.y * w;
-            v.z = v.z + part.z * w;
-            v.w = v.w + part.w * w;
+        // the parts of up to eight slots are loaded before any is added (in
+        // slot order)
+        for (int k0 = 0; k0 < topk; k0 += 8) {
+            float4 part[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int pos = k0 + j < topk ? s_pos[k0 + j] : -1;
+                part[j] = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                if (pos >= 0) part[j] = ((const float4 *)(P + (int64_t)pos * width))[d4];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (k0 + j >= topk) break;
+                const float w = s_w[k0 + j];
+                v.x = v.x + part[j].x * w;
+                v.y = v.y + part[j].y * w;
+                v.z = v.z + part[j].z * w;
+                v.w = v.w + part[j].w * w;
+            }
         }
         if (resid) {
             const float4 h = ((const float4 *)(resid + (int64_t)t * width))[d4];
@@ -945,6 +960,7 @@ inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // rows) in 16-row tiles, so the 64-row grid is not launched; larger ones
 // tile segments of more than 32 rows in 64-row tiles.
 constexpr int kSmallBatch = 64;
+constexpr int kSmallBatchColumnTiles = 2;  // column tiles per wave of the 16-row kernel up to kSmallBatch tokens
 // Largest batch whose shared-expert products run beside the router.
 constexpr int kSharedFirstMaxTokens = 1024;
 inline int tiling_split(int tokens) { return tokens <= kSmallBatch ? kSmallBatch + 1 : 33; }
@@ -1039,14 +1055,27 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
         return gate_up ? gu[kv] : dn[kv];
     };
-    auto small_kernel = [](bool gate_up, int K) -> KT {
+    // 16-row tiles: 256 weight rows per block, or 64 (one column tile per
+    // wave) for batches of up to kSmallBatch tokens, whose few tiles would
+    // otherwise leave most CUs idle (K = 640 always 256).
+    const int small_nt = tokens <= kSmallBatch ? kSmallBatchColumnTiles : 4;
+    auto small_kernel = [small_nt](bool gate_up, int K) -> KT {
         const KT gu[4] = {k_moe_gemm_rows16<true, 8>, k_moe_gemm_stream16<true, 10>, k_moe_gemm_rows16<true, 32>,
                           k_moe_gemm_rows16<true, 40>};
         const KT dn[4] = {k_moe_gemm_rows16<false, 8>, k_moe_gemm_stream16<false, 10>, k_moe_gemm_rows16<false, 32>,
                           k_moe_gemm_rows16<false, 40>};
+        const KT gu_n[4] = {k_moe_gemm_rows16<true, 8, kSmallBatchColumnTiles>, k_moe_gemm_stream16<true, 10>,
+                            k_moe_gemm_rows16<true, 32, kSmallBatchColumnTiles>,
+                            k_moe_gemm_rows16<true, 40, kSmallBatchColumnTiles>};
+        const KT dn_n[4] = {k_moe_gemm_rows16<false, 8, kSmallBatchColumnTiles>, k_moe_gemm_stream16<false, 10>,
+                            k_moe_gemm_rows16<false, 32, kSmallBatchColumnTiles>,
+                            k_moe_gemm_rows16<false, 40, kSmallBatchColumnTiles>};
         const int kv = K == 512 ? 0 : K == 640 ? 1 : K == 2048 ? 2 : 3;
+        if (small_nt != 4) return gate_up ? gu_n[kv] : dn_n[kv];
         return gate_up ? gu[kv] : dn[kv];
     };
+    // weight rows per block of the 16-row kernel for K
+    auto small_bn = [small_nt](int K) { return K == 640 ? 256 : 64 * small_nt; };
 
     // Second stream, from the start: X's hi/lo split, then (streaming shapes,
     // up to kSharedFirstMaxTokens tokens) the shared expert's gate/up and down
@@ -1073,14 +1102,14 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         rc = launched(ctx);
         if (rc == SM_OK) {
             const KT k = big ? big_kernel(true, width) : small_kernel(true, width);
-            k<<<dim3((unsigned)(2 * ff / 256), (unsigned)ntiles), 256, 0, ctx->aux>>>(
+            k<<<dim3((unsigned)(2 * ff / (big ? 256 : small_bn(width))), (unsigned)ntiles), 256, 0, ctx->aux>>>(
                 xhl, (const int *)(ws + w.rows), info_sh, tiles_sh, ar, blob_stride, sh, experts, L.gate_up_codes, L.gate_up_scales,
                 width, 2 * ff, ws + w.Hhl, ff);
             rc = launched(ctx);
         }
         if (rc == SM_OK) {
             const KT k = big ? big_kernel(false, ff) : small_kernel(false, ff);
-            k<<<dim3((unsigned)(width / 256), (unsigned)ntiles), 256, 0, ctx->aux>>>(
+            k<<<dim3((unsigned)(width / (big ? 256 : small_bn(ff))), (unsigned)ntiles), 256, 0, ctx->aux>>>(
                 hhl, nullptr, info_sh, tiles_sh, ar, blob_stride, sh, experts, L.down_codes, L.down_scales, ff, width,
                 ws + w.P, width);
             rc = launched(ctx);
@@ -1135,7 +1164,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
             }
             int rc_small = SM_OK;
             if (rc_big == SM_OK) {
-                small_kernel(gate_up, K)<<<dim3((unsigned)(N / 256), small_tiles), 256, 0, ctx->stream>>>(
+                small_kernel(gate_up, K)<<<dim3((unsigned)(N / small_bn(K)), small_tiles), 256, 0, ctx->stream>>>(
                     a, r, info_small, tiles_small, ar, blob_stride, sh, experts, codes, scales, K, N, out, ld);
                 rc_small = launched(ctx);
             }
@@ -1171,7 +1200,10 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     // before the combine reads P.
     if (int rc2 = join_aux(ctx)) return rc2;
     if (int rc2 = stage_mark(ctx, kStagePrefillCombine)) return rc2;
-    k_combine<<<(unsigned)tokens, 256, 0, ctx->stream>>>(
+    // One thread per four output columns: every load of a thread is issued
+    // at once (a 2048-wide row is two blocks).
+    const dim3 combine_grid((unsigned)tokens, (unsigned)ceil_div(width / 4, 256));
+    k_combine<<<combine_grid, 256, 0, ctx->stream>>>(
         (const float *)(ws + w.P), (const int *)(ws + w.where_), (const float *)weights, (const float *)(ws + w.gate),
         routed_rows, (float *)Y, tokens, topk, width, resid);
     if (int rc = launched(ctx)) return rc;

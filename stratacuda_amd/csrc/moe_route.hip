@@ -69,28 +69,34 @@ __global__ void __launch_bounds__(64) k_route_rows(const float *__restrict__ X, 
 }
 
 // -------------------------------------------------------- T > 1 route GEMM
-constexpr int TT = 8, TR = 8;  // tokens x rows per wave
+// Tiles of TT tokens x TR rows per wave: 8 x 8 for large batches, 4 x 4 (four
+// times the waves) for small ones.
+constexpr int kRouteSmallTileMaxTokens = 128;
 
-template <int N>
-__device__ __forceinline__ void butterfly_level(float (&a)[64], int lane) {
-    // N = number of outputs still held; keeps N/2.
+// One level of the reference's tree (lanes l and l ^ D added) over the N
+// outputs each lane still holds; lanes with bit D set keep the upper half.
+template <int N, int D>
+__device__ __forceinline__ void butterfly_level(float *a, int lane) {
     constexpr int H = N / 2;
-    const bool upper = (lane & H) != 0;
+    const bool upper = (lane & D) != 0;
 #pragma unroll
     for (int i = 0; i < H; i++) {
         float send = upper ? a[i] : a[i + H];
         float keep = upper ? a[i + H] : a[i];
-        a[i] = keep + __shfl_xor(send, H, 64);
+        a[i] = keep + __shfl_xor(send, D, 64);
     }
 }
 
-// Grid: x = row tiles (ceil((experts+1)/8)), y = token tiles (ceil(T/8)).
-// Row `experts` is the shared-expert gate. Rows/tokens past the end are
-// computed on clamped (valid) addresses and discarded.
+// Grid: x = groups of four row tiles (ceil((experts+1)/TR) tiles), y = token
+// tiles (ceil(T/TT)). Row `experts` is the shared-expert gate. Rows/tokens
+// past the end are computed on clamped (valid) addresses and discarded.
+template <int TT, int TR>
 __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X, const float *__restrict__ Wr,
                                                     const float *__restrict__ bias, const float *__restrict__ Wsg,
                                                     float *__restrict__ logits, float *__restrict__ gate_out,
                                                     int tokens, int width, int experts, int with_gate) {
+    constexpr int NO = TT * TR;  // outputs per wave
+    static_assert(NO == 64 || NO == 16, "64 or 16 outputs per wave");
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nrows = experts + (with_gate ? 1 : 0);
     const int row_tiles = (nrows + TR - 1) / TR;
@@ -108,9 +114,9 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
     }
 #pragma unroll
     for (int t = 0; t < TT; t++) xp[t] = (const char *)(X + (int64_t)min(t0 + t, tokens - 1) * width);
-    float a[64];
+    float a[NO];
 #pragma unroll
-    for (int o = 0; o < 64; o++) a[o] = 0.0f;
+    for (int o = 0; o < NO; o++) a[o] = 0.0f;
     float xv[TT], wv[TR];
     auto load = [&](uint32_t off, float *xd, float *wd) __attribute__((always_inline)) {
 #pragma unroll
@@ -124,7 +130,24 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
 #pragma unroll
             for (int r = 0; r < TR; r++) a[t * TR + r] = a[t * TR + r] + ws[r] * xs[t];
     };
-    if (width % 64 == 0) {
+    constexpr int PD = 8;  // positions in flight for the 4 x 4 tiles
+    if (NO == 16 && width % (64 * PD) == 0) {
+        // Few products per position: PD positions' values are in flight while
+        // one is used (a ring of PD buffers, refilled as each is consumed;
+        // loads past the end repeat the last position and are not used).
+        const int steps = width / 64;
+        const uint32_t first = (uint32_t)lane * 4u, last = first + (uint32_t)(steps - 1) * 256u;
+        float xb[PD][TT], wb[PD][TR];
+#pragma unroll
+        for (int p = 0; p < PD; p++) load(first + (uint32_t)p * 256u, xb[p], wb[p]);
+        for (int k = 0; k < steps; k += PD) {
+#pragma unroll
+            for (int p = 0; p < PD; p++) {
+                madd(xb[p], wb[p]);
+                load(min(first + (uint32_t)(k + p + PD) * 256u, last), xb[p], wb[p]);
+            }
+        }
+    } else if (width % 64 == 0) {
         // Each lane sums its positions lane, lane + 64, ... in order; the next
         // position's values are loaded while the current ones are used. The
         // loads are unconditional (past the end they repeat the last
@@ -148,15 +171,28 @@ __global__ void __launch_bounds__(256) k_route_gemm(const float *__restrict__ X,
             madd(xv, wv);
         }
     }
-    butterfly_level<64>(a, lane);
-    butterfly_level<32>(a, lane);
-    butterfly_level<16>(a, lane);
-    butterfly_level<8>(a, lane);
-    butterfly_level<4>(a, lane);
-    butterfly_level<2>(a, lane);
-    // lane l now holds output o = l: token t0 + l/8, row r0 + l%8.
-    const int t = t0 + lane / TR, row = r0 + lane % TR;
-    if (t < tokens && row < nrows) {
+    // The reference's tree pairs lanes at distances 32, 16, 8, 4, 2, 1.
+    int o;
+    if (NO == 64) {
+        butterfly_level<64, 32>(a, lane);
+        butterfly_level<32, 16>(a, lane);
+        butterfly_level<16, 8>(a, lane);
+        butterfly_level<8, 4>(a, lane);
+        butterfly_level<4, 2>(a, lane);
+        butterfly_level<2, 1>(a, lane);
+        o = lane;  // lane l holds output l
+    } else {
+        butterfly_level<16, 32>(a, lane);
+        butterfly_level<8, 16>(a, lane);
+        butterfly_level<4, 8>(a, lane);
+        butterfly_level<2, 4>(a, lane);
+        // lanes 4o .. 4o + 3 hold parts of output o: the last two levels
+        a[0] = a[0] + __shfl_xor(a[0], 2, 64);
+        a[0] = a[0] + __shfl_xor(a[0], 1, 64);
+        o = (lane & 3) == 0 ? lane >> 2 : NO;  // one writer per output
+    }
+    const int t = t0 + o / TR, row = r0 + o % TR;
+    if (o < NO && t < tokens && row < nrows) {
         if (row < experts) logits[(int64_t)t * experts + row] = bias ? a[0] + bias[row] : a[0];
         else gate_out[t] = a[0];
     }
@@ -467,9 +503,15 @@ int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float
         return topk_launch(ctx, logits, ids, weights, tokens, experts, topk);
     }
     const int nrows = experts + (gate_w ? 1 : 0);
-    dim3 grid((unsigned)ceil_div(ceil_div(nrows, TR), 4), (unsigned)ceil_div(tokens, TT));
-    k_route_gemm<<<grid, 256, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, tokens, width, experts,
-                                                gate_w ? 1 : 0);
+    if (tokens <= kRouteSmallTileMaxTokens) {
+        const dim3 grid((unsigned)ceil_div(ceil_div(nrows, 4), 4), (unsigned)ceil_div(tokens, 4));
+        k_route_gemm<4, 4><<<grid, 256, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, tokens, width,
+                                                          experts, gate_w ? 1 : 0);
+    } else {
+        const dim3 grid((unsigned)ceil_div(ceil_div(nrows, 8), 4), (unsigned)ceil_div(tokens, 8));
+        k_route_gemm<8, 8><<<grid, 256, 0, ctx->stream>>>(X, Wr, bias, gate_w, logits, gate_out, tokens, width,
+                                                          experts, gate_w ? 1 : 0);
+    }
     if (int rc = launched(ctx)) return rc;
     k_topk<<<(unsigned)tokens, 256, 0, ctx->stream>>>(logits, ids, weights, experts, topk);
     return launched(ctx);

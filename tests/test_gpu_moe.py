@@ -61,7 +61,8 @@ def device_inputs(backend, tokens, width, seed, normalise):
     return Xn
 
 
-@pytest.mark.parametrize("tokens,bias", [(1, False), (512, False), (2048, True)])
+@pytest.mark.parametrize("tokens,bias", [(1, False), (8, False), (9, False), (37, False), (128, True),
+                                         (129, False), (512, False), (2048, True)])
 def test_route_bit_exact(backend, oracle, full_layer, tokens, bias):
     W, E, K = wl.WIDTH, wl.EXPERTS, wl.TOPK
     X = device_inputs(backend, tokens, W, full_layer.seed + tokens, tokens == 1)
