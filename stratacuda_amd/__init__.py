@@ -289,7 +289,7 @@ class Backend:
     def moe_layer_static(self, X, tokens, Wr, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
                          weights, bias=None):
         """sm_moe_layer without a workspace: the decode path on the library's
-        static device scratch (at most 24 tokens; nothing is allocated)."""
+        static device scratch (at most 16 tokens; nothing is allocated)."""
         self._check(lib().sm_moe_layer_static(self._ctx, X.handle, tokens, Wr.handle, bias.handle if bias else 0,
                                               arena.handle, blob_stride, shared_blob.handle, Wsg.handle, width, ff,
                                               experts, topk, Y.handle, ids.handle, weights.handle))

@@ -201,7 +201,7 @@ def routing_styles(E):
 @pytest.mark.parametrize("tokens", [1, 3, 8, 20, 30])
 def test_layer_routing_edge_logits(backend, oracle, full_layer, tokens):
     # W_r = 0 makes every logit exactly the per-expert bias, so the layer's
-    # routing (the in-block top-k up to 4 tokens, the top-k kernel up to 24,
+    # routing (the in-block top-k up to 4 tokens, the top-k kernel up to 16,
     # the prefill router beyond) sees ties, underflow to 0, NaN and +-inf.
     W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
     Wr0 = backend.alloc(np.zeros(E * W, np.float32))
@@ -216,11 +216,11 @@ def test_layer_routing_edge_logits(backend, oracle, full_layer, tokens):
         assert same_bits(backend.read(w), rw), name
 
 
-@pytest.mark.parametrize("tokens", [20, 24, 25, 40, 64, 65])
+@pytest.mark.parametrize("tokens", [16, 17, 24, 25, 40, 64, 65])
 def test_layer_small_batch_full(backend, oracle, full_layer, tokens):
-    # 20 and 24 tokens: the decode kernels with a token dimension (one top-k
-    # kernel for the batch); 25..64: 16-row tiles over every segment; 65:
-    # the first batch with 64-row tiles.
+    # 16 tokens: the decode kernels with a token dimension (one top-k kernel
+    # for the batch); 17..64: 16-row tiles over every segment; 65: the first
+    # batch with 64-row tiles.
     check_full_layer(backend, oracle, full_layer, tokens, False, 6)
 
 

@@ -29,7 +29,7 @@ def _layer(backend, layers, width, ff):
     return layers[(width, ff)]
 
 
-@pytest.mark.parametrize("width,ff,token_seq", [(2048, 512, (8, 1)), (2048, 512, (24, 3)), (2560, 640, (5, 1))])
+@pytest.mark.parametrize("width,ff,token_seq", [(2048, 512, (8, 1)), (2048, 512, (16, 3)), (2560, 640, (5, 1))])
 def test_static_entry_matches_workspace_entry(backend, layers, width, ff, token_seq):
     b = backend
     E, K = wl.EXPERTS, wl.TOPK
@@ -64,12 +64,12 @@ def test_static_entry_refuses_what_does_not_fit(backend, layers):
     b = backend
     E, K = wl.EXPERTS, wl.TOPK
     lay = _layer(b, layers, 2048, 512)
-    X, Y = b.alloc(25 * 2048), b.alloc(25 * 2048)
-    ids, w = b.alloc(25 * K, "i32"), b.alloc(25 * K)
-    with pytest.raises(sm.ArgumentError, match="at most 24 tokens"):
-        b.moe_layer_static(X, 25, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 512, E, K, Y, ids, w)
-    # 24 tokens of ff 2048 need 2.3 MB of hidden rows: beyond the 2 MiB scratch
+    X, Y = b.alloc(17 * 2048), b.alloc(17 * 2048)
+    ids, w = b.alloc(17 * K, "i32"), b.alloc(17 * K)
+    with pytest.raises(sm.ArgumentError, match="at most 16 tokens"):
+        b.moe_layer_static(X, 17, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 512, E, K, Y, ids, w)
+    # 16 tokens of ff 3072 need 2.2 MiB of decode scratch: beyond the 2 MiB array
     with pytest.raises(sm.ArgumentError, match="static scratch holds"):
-        b.moe_layer_static(X, 24, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 2048, E, K, Y, ids, w)
+        b.moe_layer_static(X, 16, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 3072, E, K, Y, ids, w)
     for buf in (X, Y, ids, w):
         b.free(buf)
