@@ -431,10 +431,16 @@ def _gemm_label(name):
     if m:
         return "k_moe_gemm_stream<%s, %d x %d tile, K/64 = %s>" % (
             "gate_up" if m.group(1) == "1" else "down", 32 * int(m.group(2)), 128 * int(m.group(3)), m.group(4))
-    m = re.search(r"k_moe_gemm_(stream16|rows16)ILb(\d)ELi(\d+)E", name)
-    if m:
-        return "k_moe_gemm_%s<%s, 16 x 256 tile, K/64 = %s>" % (m.group(1), "gate_up" if m.group(2) == "1" else "down",
-                                                               m.group(3))
+    # 16-row kernels: weight rows per block 64 x NT (the rows16 kernel's third
+    # template argument, 4 when absent), mangled or demangled
+    m = re.search(r"k_moe_gemm_(stream16|rows16)ILb(\d)ELi(\d+)E(?:Li(\d)E)?", name)
+    g = (m.group(1), m.group(2) == "1", m.group(3), m.group(4)) if m else None
+    if not m:
+        m = re.search(r"k_moe_gemm_(stream16|rows16)<(true|false), (\d+)(?:, (\d))?>", name)
+        g = (m.group(1), m.group(2) == "true", m.group(3), m.group(4)) if m else None
+    if g:
+        return "k_moe_gemm_%s<%s, 16 x %d tile, K/64 = %s>" % (g[0], "gate_up" if g[1] else "down",
+                                                              64 * int(g[3] or 4), g[2])
     m = re.search(r"k_split_hilo", name)
     if m:
         return "k_split_hilo"
