@@ -868,7 +868,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     __shared__ int s_ids[32];
     __shared__ float s_w[32];
     __shared__ float s_parts[(kFusedMaxTopk + 2) * 8];
-    __shared__ __attribute__((aligned(16))) float s_h[kFusedWaves][8 * DN_PITCH];
+    __shared__ __attribute__((aligned(16))) float s_h[kFusedWaves][2][8 * DN_PITCH];
     __shared__ uint32_t s_arrive;
     __shared__ int s_ok;
     __shared__ float s_logit[512];
@@ -1090,7 +1090,6 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     __syncthreads();
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
         a.hidden, (short)0, (int)((uint32_t)nslot * kFusedFF * 4), 0x00020000);
-    float *xh = s_h[wave];
     // lane (rr, g8) brings values 8 rr .. 8 rr + 7 of hidden group g8 of each
     // of the wave's slots; all loads issued before any is used (a slot past
     // the last reads the last one again)
@@ -1104,37 +1103,69 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     }
     const float shared_gate = load_coherent(a.gate);
     if (wave == 0) FUSED_MARK_LOADED(11);
+    // The wave's slots are wave and wave + 8 (two for waves 0-2 at top-10);
+    // with two, both dots run side by side (independent chains), each slot
+    // with its own exchange area. Per slot: the group sum of the hidden
+    // values (own eighth, then lanes ^ 8, ^ 16, ^ 32), the exchange (lane
+    // (rr, g8) stores values 8 rr .. 8 rr + 7 of group g8, then reads the
+    // whole group), the dot in dot64_4's order.
+    const bool two = wave + kFusedWaves < nslot;
+    float s8[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < 2; q++) {
-        const int s = wave + kFusedWaves * q;
-        if (s >= nslot) break;
+        if (q == 1 && !two) break;
         const float4 h0 = hq[q][0], h1 = hq[q][1];
-        float s8 = ((h0.x + h0.y) + (h0.z + h0.w)) + ((h1.x + h1.y) + (h1.z + h1.w));
-        s8 = s8 + sm::dpp_f32<0x128>(0.0f, s8);
-        {
-            const int u = __builtin_bit_cast(int, s8);
-            const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-            s8 = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
-            const int w = __builtin_bit_cast(int, s8);
-            const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-            s8 = __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
-        }
+        float t = ((h0.x + h0.y) + (h0.z + h0.w)) + ((h1.x + h1.y) + (h1.z + h1.w));
+        t = t + sm::dpp_f32<0x128>(0.0f, t);
+        const int u = __builtin_bit_cast(int, t);
+        const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        t = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
+        const int w = __builtin_bit_cast(int, t);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+        s8[q] = __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
+        float *xh = s_h[wave][q];
         *(float4 *)&xh[g8 * DN_PITCH + 8 * rr] = h0;
         *(float4 *)&xh[g8 * DN_PITCH + 8 * rr + 4] = h1;
-        __builtin_amdgcn_wave_barrier();
-        float hv[64];
+    }
+    __builtin_amdgcn_wave_barrier();
+    // 16 hidden values of group g8 (chunk w4) from exchange area q
+    auto chunk = [&](int q, int w4, float (&x)[16]) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float4 v = *(const float4 *)&xh[g8 * DN_PITCH + 4 * i];
-            hv[4 * i] = v.x;
-            hv[4 * i + 1] = v.y;
-            hv[4 * i + 2] = v.z;
-            hv[4 * i + 3] = v.w;
+        for (int i = 0; i < 4; i++) {
+            const float4 v = *(const float4 *)&s_h[wave][q][g8 * DN_PITCH + 16 * w4 + 4 * i];
+            x[4 * i] = v.x;
+            x[4 * i + 1] = v.y;
+            x[4 * i + 2] = v.z;
+            x[4 * i + 3] = v.w;
         }
-        __builtin_amdgcn_wave_barrier();
-        float v = dok[q] ? sm::half_bits(dsb[q]) * (dot64_4(dc[q], hv) - s8) : __builtin_nanf("");
+    };
+    auto word = [](const uint4 &c, int w4) { return w4 == 0 ? c.x : w4 == 1 ? c.y : w4 == 2 ? c.z : c.w; };
+    float d[2][4];
+    if (two) {
+#pragma unroll
+        for (int w4 = 0; w4 < 4; w4++) {
+            float x0[16], x1[16];
+            chunk(0, w4, x0);
+            chunk(1, w4, x1);
+            d[0][w4] = dot16(word(dc[0], w4), x0, 0.0f);
+            d[1][w4] = dot16(word(dc[1], w4), x1, 0.0f);
+        }
+    } else {
+#pragma unroll
+        for (int w4 = 0; w4 < 4; w4++) {
+            float x0[16];
+            chunk(0, w4, x0);
+            d[0][w4] = dot16(word(dc[0], w4), x0, 0.0f);
+            d[1][w4] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        if (q == 1 && !two) break;
+        const float dot = (d[q][0] + d[q][1]) + (d[q][2] + d[q][3]);
+        float v = dok[q] ? sm::half_bits(dsb[q]) * (dot - s8[q]) : __builtin_nanf("");
         v = sm::group8_sum(v);
-        if (g8 == 0) s_parts[s * 8 + rr] = v;
+        if (g8 == 0) s_parts[(wave + kFusedWaves * q) * 8 + rr] = v;
     }
     __syncthreads();
     if (tid < 8) {
