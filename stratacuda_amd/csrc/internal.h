@@ -90,7 +90,7 @@ enum Stage {
     kStageCount = 9
 };
 int stage_mark(sm_ctx *ctx, int stage);
-constexpr int kCounterWords = 4096;
+constexpr int kCounterWords = 16384;
 constexpr int kFusedSyncBase = 1024;
 // Index in ctx->counters of the fused decode layer's sticky fault word.
 uint32_t fused_fault_word();

@@ -737,14 +737,23 @@ constexpr int kFusedWidth = 2048, kFusedFF = 512, kFusedMaxTopk = 10;
 constexpr int kFusedCollector = kFusedBlocks - 1;  // block whose wave 7 collects the flags
 constexpr uint32_t kFusedSpinLimit = 1u << 20;
 // Word offsets in the synchronisation area (ctx->counters + kFusedSyncBase):
-// the flags of hand-off B (one word per block), then the go word and the
-// fault word on lines of their own.
-constexpr int kFusedFlagsB = 0, kFusedGoB = kFusedBlocks + 32, kFusedFaultWord = kFusedGoB + 32;
-// The tagged logits (two words per expert, 8-byte aligned), in the same area
-// so that only this kernel ever writes them: a stale tag is an earlier
+// the flags of hand-off B (one word per block) and the fault word on a line
+// of its own, then kFusedGoCopies copies of the go word, one per 128-byte
+// line, and kFusedLogitCopies copies of the tagged logits (two words per
+// expert, 4 KiB per copy). Block b polls go copy b % kFusedGoCopies and
+// logit copy b % kFusedLogitCopies: polls of 256 blocks on one line queue at
+// its memory channel, copies spread them. The tagged logits live in this
+// area so that only this kernel ever writes them: a stale tag is an earlier
 // launch's number, never the current one.
-constexpr int kFusedLogitWords = 512;
-constexpr int kFusedSyncWords = kFusedLogitWords + 2 * 512;
+constexpr int kFusedGoCopies = 8, kFusedLogitCopies = 8;
+constexpr int kFusedFlagsB = 0, kFusedFaultWord = kFusedBlocks + 32;
+constexpr int kFusedGoB = 512, kFusedLogitWords = kFusedGoB + kFusedGoCopies * 32;
+constexpr int kFusedSyncWords = kFusedLogitWords + kFusedLogitCopies * 1024;
+static_assert(kFusedGoCopies <= kFusedBlocks && kFusedLogitCopies <= 64, "copies");
+__device__ __forceinline__ uint32_t *fused_go(uint32_t *sync, int copy) { return sync + kFusedGoB + copy * 32; }
+// tagged logit of expert e in copy c (logits = sync + kFusedLogitWords as
+// 8-byte words)
+__device__ __forceinline__ uint64_t *fused_logit(uint64_t *logits, int c, int e) { return logits + c * 512 + e; }
 
 struct FusedArgs {
     const float *X, *Wr, *bias, *Wsg, *gamma;
@@ -804,8 +813,8 @@ __device__ bool wait_go(uint32_t *go, uint32_t launch, uint32_t *fault) {
     return false;
 }
 // The collector: one wave reads the 256 flags of a phase (4 per lane) until
-// all hold `launch`, then publishes `launch` in the go word.
-__device__ bool collect(uint32_t *flags, uint32_t *go, uint32_t launch, uint32_t *fault) {
+// all hold `launch`, then publishes `launch` in every copy of the go word.
+__device__ bool collect(uint32_t *flags, uint32_t *sync, uint32_t launch, uint32_t *fault) {
     const uint32_t want = (uint32_t)__builtin_amdgcn_readfirstlane((int)launch);
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(flags, (short)0, kFusedBlocks * 4, 0x00020000);
     const uint32_t off = (uint32_t)(threadIdx.x & 63) * 16;
@@ -815,7 +824,8 @@ __device__ bool collect(uint32_t *flags, uint32_t *go, uint32_t launch, uint32_t
                         (int)(f.w - want) >= 0;
         if (__ballot(!in) == 0) {
             loads_ordered();
-            if ((threadIdx.x & 63) == 0) __hip_atomic_store(go, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int c = threadIdx.x & 63; c < kFusedGoCopies; c += 64)
+                __hip_atomic_store(fused_go(sync, c), want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return true;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -880,7 +890,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     uint32_t *fault = a.sync + kFusedFaultWord;
     // This launch's number: the go word as the previous launch left it, plus
     // one (consumed only by the tags, flags and waits).
-    const uint32_t launch = load_coherent_u32(a.sync + kFusedGoB) + 1u;
+    const uint32_t launch = load_coherent_u32(fused_go(a.sync, b % kFusedGoCopies)) + 1u;
     // LDS holds garbage at launch: the arrival counter is cleared before any
     // wave can use it.
     if (tid == 0) s_arrive = 0;
@@ -931,8 +941,10 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         sum = sm::tree_sum64(sum);
         if (lane == 0 && row < experts) {
             const float logit = a.bias ? sum + rbias : sum;
-            __hip_atomic_store(a.logits + row, ((uint64_t)launch << 32) | __builtin_bit_cast(uint32_t, logit),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t tagged = ((uint64_t)launch << 32) | __builtin_bit_cast(uint32_t, logit);
+#pragma unroll
+            for (int c = 0; c < kFusedLogitCopies; c++)
+                __hip_atomic_store(fused_logit(a.logits, c, row), tagged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         if (wave == 0) FUSED_MARK(2);
     } else {
@@ -971,7 +983,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                t[j] = __hip_atomic_load(a.logits + min(lane + 64 * j, experts - 1), __ATOMIC_RELAXED,
+                t[j] = __hip_atomic_load(fused_logit(a.logits, b % kFusedLogitCopies, min(lane + 64 * j, experts - 1)), __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
             bool mine = true;
 #pragma unroll
@@ -1080,11 +1092,11 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         dsb[q] = *(const uint16_t *)(blob + a.down_scales + ((uint64_t)drow * GD + g8) * 2);
     }
     if (b == kFusedCollector && wave == kFusedWaves - 1 && ok)
-        collect(a.sync + kFusedFlagsB, a.sync + kFusedGoB, launch, fault);
+        collect(a.sync + kFusedFlagsB, a.sync, launch, fault);
 
     // ---- phase B wait; then the block's 8 output rows.
     if (wave == 0) {
-        if (ok) ok = wait_go(a.sync + kFusedGoB, launch, fault);
+        if (ok) ok = wait_go(fused_go(a.sync, b % kFusedGoCopies), launch, fault);
         FUSED_MARK(8);
     }
     __syncthreads();
