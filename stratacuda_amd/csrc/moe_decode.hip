@@ -1114,6 +1114,11 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         hq[q][1] = load16_coherent(hr, off + 16);
     }
     const float shared_gate = load_coherent(a.gate);
+    // Read with the hidden rows rather than after the products: a wait that
+    // gave up in any block set the fault word before that block's flag, so
+    // before the go word; this block's own give-ups are in wave 0's `ok`
+    // (wave 0 forms the outputs).
+    const bool faulted = load_coherent_u32(fault) != 0u || !ok;
     if (wave == 0) FUSED_MARK_LOADED(11);
     // The wave's slots are wave and wave + 8 (two for waves 0-2 at top-10);
     // with two, both dots run side by side (independent chains), each slot
@@ -1185,7 +1190,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         const float sig = sm::sigmoid(shared_gate, s_tab);
         float value = s_parts[topk * 8 + tid] * sig;
         for (int k = 0; k < topk; k++) value = value + s_parts[k * 8 + tid] * s_w[k];
-        if (load_coherent_u32(fault) != 0u) value = __builtin_nanf("");
+        if (faulted) value = __builtin_nanf("");
         a.Y[r] = NORM ? xres + value : value;
     }
     if (wave == 0) FUSED_MARK(9);
