@@ -852,13 +852,30 @@ __device__ __forceinline__ void load_xq_lds(const uint32_t *rec, int g, XQ &q) {
     q.sum = (int)rec[g * kRecPitch + 49];
 }
 
+// Whole-wave wait for a block-local LDS flag set by another wave of the
+// block (a relaxed store after a release fence): once the flag reads
+// non-zero, the LDS writes made before it are visible.
+__device__ __forceinline__ void lds_wait(int *flag) {
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The same for a count that `n` waves raise by one each.
+__device__ __forceinline__ void lds_wait_count(int *count, int n) {
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < n)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Timeline hook, compiled in only with -DSM_FUSED_TRACE (profiling builds):
 // lane 0 of the calling wave records the real-time clock (100 MHz) at mark k
-// of its block.
+// of its block in LDS (no memory store that a later wait would cover); the
+// block's marks go to g_fused_trace when it ends.
 #ifdef SM_FUSED_TRACE
-__device__ uint64_t g_fused_trace[kFusedBlocks * 16];
+__device__ uint64_t g_fused_trace[kFusedBlocks * 32];
 #define FUSED_MARK(k) \
-    do { if ((threadIdx.x & 63) == 0) g_fused_trace[blockIdx.x * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+    do { if ((threadIdx.x & 63) == 0) s_marks[k] = __builtin_amdgcn_s_memrealtime(); } while (0)
 // the same once the wave's outstanding loads are in (profiling builds only)
 #define FUSED_MARK_LOADED(k) \
     do { __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8)); FUSED_MARK(k); } while (0)
@@ -870,7 +887,7 @@ __device__ uint64_t g_fused_trace[kFusedBlocks * 16];
 #endif
 
 template <bool NORM>
-__global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs a) {
+__global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs a) {
     constexpr int G = kFusedWidth / 64, GD = kFusedFF / 64, ROW_BYTES = kFusedWidth / 4;
     __shared__ __attribute__((aligned(16))) uint32_t s_rec[G * kRecPitch];
     __shared__ uint64_t s_tab[32];
@@ -880,8 +897,11 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     __shared__ float s_parts[(kFusedMaxTopk + 2) * 8];
     __shared__ __attribute__((aligned(16))) float s_h[kFusedWaves][2][8 * DN_PITCH];
     __shared__ uint32_t s_arrive;
-    __shared__ int s_ok;
+    __shared__ int s_ok, s_spec, s_reload, s_staged, s_selected, s_recs;
     __shared__ float s_logit[512];
+#ifdef SM_FUSED_TRACE
+    __shared__ uint64_t s_marks[32];
+#endif
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.x, gw = b * kFusedWaves + wave;
@@ -893,7 +913,12 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     const uint32_t launch = load_coherent_u32(fused_go(a.sync, b % kFusedGoCopies)) + 1u;
     // LDS holds garbage at launch: the arrival counter is cleared before any
     // wave can use it.
-    if (tid == 0) s_arrive = 0;
+    if (tid == 0) {
+        s_arrive = 0;
+        s_staged = 0;
+        s_selected = 0;
+        s_recs = 0;
+    }
     __syncthreads();
     bool ok = true;
     if (wave == 0) FUSED_MARK(0);
@@ -964,6 +989,12 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
                 s_rec[g * kRecPitch + 49] = (uint32_t)sum;
             }
         }
+        // this wave's records are written: counted for the waves that load
+        // them before the block's next barrier
+        if (lane == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __hip_atomic_fetch_add(&s_recs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         if (wave == 2) FUSED_MARK(1);
         if (gate_wave) {
             float gs = 0.0f;
@@ -975,16 +1006,27 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
     }
 
     // ---- hand-off A: wave 0 polls the tagged logits until all are this
-    // launch's, and stages them in LDS; then every block routes the token
-    // itself (router_block512: one exponential per thread, wave 0 selects).
+    // launch's, stages them in LDS and picks the top-k by logit (the
+    // reference's selection in all but near-tie cases); every wave issues its
+    // phase-B code loads for those experts at once, forms one exponential,
+    // and wave 0 then confirms the selection from the probabilities (or
+    // replaces it, and the loads are issued again).
     if (wave == 0) {
-        uint64_t t[8];
-        bool all = false;
-        for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+        // One round reads all 512 tagged words of this block's copy. While
+        // the next round is in flight, the selection threshold is searched
+        // over the logits already in (valid for the complete set), which
+        // takes the search off the path after the last round.
+        auto poll = [&](uint64_t (&d)[8]) {
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                t[j] = __hip_atomic_load(fused_logit(a.logits, b % kFusedLogitCopies, min(lane + 64 * j, experts - 1)), __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
+                d[j] = __hip_atomic_load(fused_logit(a.logits, b % kFusedLogitCopies, min(lane + 64 * j, experts - 1)),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        };
+        uint64_t t[8];
+        poll(t);
+        bool all = false;
+        uint32_t T0 = 0;
+        for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
             bool mine = true;
 #pragma unroll
             for (int j = 0; j < 8; j++) mine = mine && (uint32_t)(t[j] >> 32) == launch;
@@ -992,25 +1034,92 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
                 all = true;
                 break;
             }
+            uint64_t tn[8];
+            poll(tn);
+            uint32_t hk = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const bool cur = (uint32_t)(t[j] >> 32) == launch && lane + 64 * j < experts;
+                hk = max(hk, cur ? sm::logit_key(__builtin_bit_cast(float, (uint32_t)t[j])) : 0u);
+            }
+            T0 = max(T0, sm::logit_threshold(hk, topk));
             __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < 8; j++) t[j] = tn[j];
         }
         if (!all) set_fault(fault);
         ok = all;
+        float lg[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            s_logit[lane + 64 * j] = lane + 64 * j < experts ? __builtin_bit_cast(float, (uint32_t)t[j]) : -3.402823e38f;
+        for (int j = 0; j < 8; j++) {
+            lg[j] = lane + 64 * j < experts ? __builtin_bit_cast(float, (uint32_t)t[j]) : -3.402823e38f;
+            s_logit[lane + 64 * j] = lg[j];
+        }
+        if (lane == 0) {
+            s_ok = ok;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __hip_atomic_store(&s_staged, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         FUSED_MARK(3);
-        if (lane == 0) s_ok = ok;
+        const bool spec = sm::select_by_logit(lg, experts, topk, T0, s_router, s_ids);
+        // without a candidate the first loads read experts 0..topk-1 (in
+        // bounds; replaced once the selection is made)
+        if (!spec && lane < topk) s_ids[lane] = lane;
+        if (lane == 0) {
+            s_spec = spec;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __hip_atomic_store(&s_selected, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
     }
-    __syncthreads();
-    ok = s_ok;
-    {
+    // Wave 1 forms the probabilities meanwhile (the logits staged by wave 0).
+    float prob[8];
+    if (wave == 1) {
+        lds_wait(&s_staged);
         float lg[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) lg[j] = s_logit[lane + 64 * j];
-        sm::router_block512(lg, experts, topk, s_tab, s_router, s_ids);
+        sm::router_probs_wave(lg, experts, s_tab, s_router, prob);
     }
-    if (wave == 0) {
+    // Every wave waits for the candidate IDs (LDS flag, no barrier: wave 1
+    // may still be forming probabilities) and issues its phase-B code loads.
+    // Nothing earlier is outstanding by now (the wait tells the compiler so,
+    // which keeps it from waiting for everything before the first code load).
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0)
+    if (wave != 0) lds_wait(&s_selected);
+    if (wave == 0) FUSED_MARK(12);
+    ok = s_ok;
+
+    // ---- phase B: kFusedRows hidden rows of the 11 x 512 (item = slot x 512
+    // + row; the shared expert is slot topk). Code loads from s_ids.
+    const int rr = lane >> 3, g8 = lane & 7;
+    const int drow = b * 8 + rr;
+    uint4 c[kFusedRows];
+    uint32_t sb[kFusedRows];
+    bool rok[kFusedRows];
+    auto issue_codes = [&]() {
+#pragma unroll
+        for (int r = 0; r < kFusedRows; r++) {
+            const int item = min(gw * kFusedRows + r, nslot * kFusedFF - 1);
+            const int k = item / kFusedFF, j = item - k * kFusedFF;
+            const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, k < topk ? s_ids[k] : 0, k, topk, experts);
+            rok[r] = blob != nullptr;
+            blob = blob ? blob : a.shared;
+            const uint64_t wrow = 2 * (uint64_t)j + half;
+            c[r] = load_codes(blob + wrow * ROW_BYTES + gl * 16);
+            sb[r] = *(const uint16_t *)(blob + a.gu_scales + (wrow * G + gl) * 2);
+        }
+    };
+    issue_codes();
+    // The activation records of the lane's group into registers while the
+    // codes are in flight (once the six record waves have written them).
+    lds_wait_count(&s_recs, kFusedWaves - 2);
+    XQ xq;
+    load_xq_lds(s_rec, gl, xq);
+    // Wave 1 confirms the candidate from the probabilities (or replaces it:
+    // the loads are then issued again) and forms the weights; the barrier
+    // orders LDS only, so every wave's code loads stay in flight.
+    if (wave == 1) {
+        const bool stood = sm::router_confirm(prob, experts, topk, s_spec, s_router, s_ids);
         FUSED_MARK(4);
         sm::wave_lds_sync();
         // weights = selected / max(sum of selected, 2^-14), sum in k order
@@ -1025,35 +1134,16 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
                 a.weights[lane] = wk;
             }
         }
+        if (lane == 0) s_reload = !stood;
     }
-    __syncthreads();
+    sm::lds_barrier();
     if (wave == 0) FUSED_MARK(5);
-
-    // ---- phase B: kFusedRows hidden rows of the 11 x 512 (item = slot x 512
-    // + row; the shared expert is slot topk).
-    const int rr = lane >> 3, g8 = lane & 7;
-    const int drow = b * 8 + rr;
+    if (s_reload) issue_codes();
     {
-        uint4 c[kFusedRows];
-        uint32_t sb[kFusedRows];
-        bool rok[kFusedRows];
-#pragma unroll
-        for (int r = 0; r < kFusedRows; r++) {
-            const int item = min(gw * kFusedRows + r, nslot * kFusedFF - 1);
-            const int k = item / kFusedFF, j = item - k * kFusedFF;
-            const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, k < topk ? s_ids[k] : 0, k, topk, experts);
-            rok[r] = blob != nullptr;
-            blob = blob ? blob : a.shared;
-            const uint64_t wrow = 2 * (uint64_t)j + half;
-            c[r] = load_codes(blob + wrow * ROW_BYTES + gl * 16);
-            sb[r] = *(const uint16_t *)(blob + a.gu_scales + (wrow * G + gl) * 2);
-        }
-        if (wave == 0) FUSED_MARK_LOADED(10);
-        XQ q;
-        load_xq_lds(s_rec, gl, q);
+        FUSED_MARK_LOADED(16 + wave);
         float acc[kFusedRows];
 #pragma unroll
-        for (int r = 0; r < kFusedRows; r++) acc[r] = sm::half_bits(sb[r]) * dot64_q(c[r], q);
+        for (int r = 0; r < kFusedRows; r++) acc[r] = sm::half_bits(sb[r]) * dot64_q(c[r], xq);
         // row r's gate and up sums (lanes 31 and 63) go to lane r: one SiLU
         float g = 0.0f, u = 0.0f;
 #pragma unroll
@@ -1072,8 +1162,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         if (lane < kFusedRows && item < nslot * kFusedFF) store_coherent(a.hidden + item, h);
     }
     stores_complete();
-    if (wave == 0) FUSED_MARK(6);
-    if (wave == 7) FUSED_MARK(7);
+    FUSED_MARK(24 + wave);
     // the block's flag once all eight waves are done
     if (lane == 0 && atomicAdd(&s_arrive, 1u) == kFusedWaves - 1)
         __hip_atomic_store(a.sync + kFusedFlagsB + b, launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1091,8 +1180,10 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         dc[q] = load_codes(blob + a.down_codes + (uint64_t)drow * (kFusedFF / 4) + g8 * 16);
         dsb[q] = *(const uint16_t *)(blob + a.down_scales + ((uint64_t)drow * GD + g8) * 2);
     }
-    if (b == kFusedCollector && wave == kFusedWaves - 1 && ok)
+    if (b == kFusedCollector && wave == kFusedWaves - 1 && ok) {
         collect(a.sync + kFusedFlagsB, a.sync, launch, fault);
+        FUSED_MARK(13);
+    }
 
     // ---- phase B wait; then the block's 8 output rows.
     if (wave == 0) {
@@ -1194,6 +1285,10 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 2) k_decode_fused(FusedArgs 
         a.Y[r] = NORM ? xres + value : value;
     }
     if (wave == 0) FUSED_MARK(9);
+#ifdef SM_FUSED_TRACE
+    __syncthreads();
+    if (tid < 32) g_fused_trace[b * 32 + tid] = s_marks[tid];
+#endif
 }
 
 constexpr uint64_t kAlign = 256;
@@ -1249,8 +1344,8 @@ static_assert((kFusedSyncBase + kFusedLogitWords) % 2 == 0, "tagged logits are 8
 
 #ifdef SM_FUSED_TRACE
 extern "C" int sm_fused_trace_read(uint64_t *out, int n) {
-    if (n < kFusedBlocks * 16) return SM_E_ARG;
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_fused_trace), sizeof(uint64_t) * kFusedBlocks * 16) == hipSuccess
+    if (n < kFusedBlocks * 32) return SM_E_ARG;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_fused_trace), sizeof(uint64_t) * kFusedBlocks * 32) == hipSuccess
                ? SM_OK
                : SM_E_HIP;
 }

@@ -497,6 +497,15 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A block barrier that orders LDS accesses only: each wave's LDS accesses
+// complete before the barrier, and its outstanding global loads and stores
+// stay in flight (__syncthreads waits for those too).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // LDS for router_block: probabilities, the cross-wave max, and the scratch of
 // select_ranked.
 struct RouterScratch {
@@ -505,6 +514,58 @@ struct RouterScratch {
     alignas(16) uint64_t cand[128];  // up to 64 candidates, zeros after the last (read 8 at a time)
     float val[32];
 };
+
+// Gathers the entries with in[j] set (at most 64, else returns false and
+// writes nothing) into x.cand, one per lane, and ranks each against the
+// others by its packed key Q = order key << 9 | (511 - e): the entry of rank
+// k (k < topK) goes to s_ids[k], and with `with_val` its key's upper 32 bits,
+// read back as a probability, to x.val[k]. Lane l's entries land after the
+// entries of lanes 0..l-1 (a lane scan of the per-lane counts, all on the
+// vector unit); the slots after the last hold 0, below every candidate.
+__device__ __forceinline__ bool rank_candidates(const uint64_t (&Q)[8], const bool (&in)[8], int topK,
+                                                RouterScratch &x, int *s_ids, bool with_val) {
+    const int lane = threadIdx.x & 63;
+    int pos[8], n = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        pos[j] = n;
+        n += in[j] ? 1 : 0;
+    }
+    const int incl = wave_scan_incl(n);
+    const int count = __builtin_amdgcn_readlane(incl, 63);
+    if (count > 64) return false;
+    x.cand[lane] = 0ull;
+    // entries that are not candidates go to slot 64 + lane, never read
+#pragma unroll
+    for (int j = 0; j < 8; j++) x.cand[in[j] ? incl - n + pos[j] : 64 + lane] = Q[j];
+    wave_lds_sync();
+    // Candidate `lane` against every candidate: 8 at a time through
+    // broadcast 16-byte LDS reads (every lane reads the same address).
+    // Slots 0..15 always (those past `count` hold 0, below every candidate),
+    // then 8 at a time; four partial counts keep the additions independent.
+    const uint64_t q = x.cand[lane];
+    int rk[4] = {0, 0, 0, 0};
+    auto rank8 = [&](int c) {
+        const uint4 *src = (const uint4 *)&x.cand[c];
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = src[u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint64_t a = ((uint64_t)v[u].y << 32) | v[u].x, b = ((uint64_t)v[u].w << 32) | v[u].z;
+            rk[u] += (a > q ? 1 : 0) + (b > q ? 1 : 0);
+        }
+    };
+    rank8(0);
+    rank8(8);
+    for (int c = 16; c < count; c += 8) rank8(c);
+    const int rank = (rk[0] + rk[1]) + (rk[2] + rk[3]);
+    if (lane < count && rank < topK) {
+        s_ids[rank] = 511 - (int)(q & 511u);
+        if (with_val) x.val[rank] = __builtin_bit_cast(float, (uint32_t)(q >> 9) ^ 0x80000000u);
+    }
+    return true;
+}
 
 // The same selection as select_rounds in one pass. Entry e gets the 41-bit
 // order key Q = (key ^ 2^31) << 9 | (511 - e): Q descending is exactly the
@@ -542,52 +603,17 @@ __device__ __forceinline__ void select_ranked(const int (&key)[8], int experts, 
         const uint32_t c = T | (1u << b);
         if (popc64(__ballot(hk >= c)) >= topK) T = c;
     }
-    // Candidates: entries with key >= T. Lane l's candidates go to cand[]
-    // from its exclusive prefix (a lane scan of the per-lane counts, all on
-    // the vector unit); the slots after the last hold 0, below every
-    // candidate (a candidate's key has its top bit set).
     uint64_t Q[8];
     bool in[8];
-    int pos[8], n = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const uint32_t k = (uint32_t)key[j] ^ 0x80000000u;
         Q[j] = ((uint64_t)k << 9) | (uint64_t)(511 - (lane + 64 * j));
         in[j] = k >= T;
-        pos[j] = n;
-        n += in[j] ? 1 : 0;
     }
-    const int incl = wave_scan_incl(n);
-    const int count = __builtin_amdgcn_readlane(incl, 63);
-    if (count > 64) {
+    if (!rank_candidates(Q, in, topK, x, s_ids, true)) {
         select_rounds(key, experts, topK, s_ids, mine);
         if (lane < topK) x.val[lane] = mine;
-        return;
-    }
-    x.cand[lane] = 0ull;
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (in[j]) x.cand[incl - n + pos[j]] = Q[j];
-    wave_lds_sync();
-    // Candidate `lane` against every candidate: 8 at a time through
-    // broadcast 16-byte LDS reads (every lane reads the same address).
-    const uint64_t q = x.cand[lane];
-    int rank = 0;
-    for (int c = 0; c < count; c += 8) {
-        const uint4 *src = (const uint4 *)&x.cand[c];
-        uint4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = src[u];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint64_t a = ((uint64_t)v[u].y << 32) | v[u].x, b = ((uint64_t)v[u].w << 32) | v[u].z;
-            rank += (a > q ? 1 : 0) + (b > q ? 1 : 0);
-        }
-    }
-    // the round-`rank` winner: its ID and probability straight into place
-    if (lane < count && rank < topK) {
-        s_ids[rank] = 511 - (int)(q & 511u);
-        x.val[rank] = __builtin_bit_cast(float, (uint32_t)(q >> 9) ^ 0x80000000u);
     }
 }
 
@@ -640,10 +666,12 @@ __device__ __forceinline__ void router_block(const float (&l)[8], int experts, i
     if (wave != 0) return;
     router_select_lds(experts, topK, s, s_ids);
 }
-// The same with 512 threads (8 waves): thread t forms expert t's exponential.
-// Needs blockDim.x == 512 and experts <= 512.
-__device__ __forceinline__ void router_block512(const float (&l)[8], int experts, int topK, const uint64_t *s_tab,
-                                                RouterScratch &s, int *s_ids) {
+// The exponentials of a 512-thread block (8 waves): thread t forms expert
+// t's exp(l - max) in s.p[t] (+0 past `experts`); every wave forms the
+// maximum itself from its copy of the logits. No barrier: the caller's makes
+// s.p visible. s_tab must already hold kExp2Tab.
+__device__ __forceinline__ void router_exps512(const float (&l)[8], int experts, const uint64_t *s_tab,
+                                               RouterScratch &s) {
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     float mx = l[0];
@@ -658,8 +686,14 @@ __device__ __forceinline__ void router_block512(const float (&l)[8], int experts
     float ex[1];
     expf_or_n<1>(d, ex, s_tab);
     s.p[tid] = tid < experts ? ex[0] : 0.0f;
+}
+// The same routing as router_block with 512 threads: thread t forms expert
+// t's exponential. Needs blockDim.x == 512 and experts <= 512.
+__device__ __forceinline__ void router_block512(const float (&l)[8], int experts, int topK, const uint64_t *s_tab,
+                                                RouterScratch &s, int *s_ids) {
+    router_exps512(l, experts, s_tab, s);
     __syncthreads();
-    if (wave != 0) return;
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) != 0) return;
     router_select_lds(experts, topK, s, s_ids);
 }
 // Wave 0's part of router_block / router_block512: the reference sum of the
@@ -681,6 +715,133 @@ __device__ __forceinline__ void router_select_lds(int experts, int topK, RouterS
     // IDs into s_ids, selected probabilities into s.val (for router_weights
     // once the block has issued its expert loads: the IDs alone gate those)
     select_ranked(key, experts, topK, s, s_ids);
+}
+
+// ---------------------------------------------------------- routing by logit
+// A routing split in two so that expert loads need not wait for the
+// exponentials. Probabilities are p = fl(fl(expf(l - max)) * inv), each step
+// non-decreasing in l for every l where the rounding of expf is monotone, so
+// the reference's selection (kernels/strata.cu:255-265: p descending, lower
+// ID on ties) is nearly always the top-topK by (logit descending, lower ID);
+// select_by_logit finds that candidate from the logits alone, and
+// router_confirm_lds later proves or replaces it from the probabilities.
+//
+// Order key of a logit: its bits mapped so that unsigned comparison orders
+// like the values (negative values reversed; NaNs at either end).
+__device__ __forceinline__ uint32_t logit_key(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// The selection threshold over one wave's lane maxima hk (logit keys, 0 for
+// none): the largest T whose bits 31..18 are set greedily such that at least
+// topK lanes have hk >= T, as in select_ranked. Any T at or below the topK-th
+// largest lane maximum keeps every one of the topK largest entries at or
+// above it, and so does a T found over a subset of the entries. Returns 0
+// when fewer than topK lanes hold an entry.
+__device__ __forceinline__ uint32_t logit_threshold(uint32_t hk, int topK) {
+    if (popc64(__ballot(hk != 0u)) < topK) return 0u;
+    uint32_t T = 0;
+#pragma unroll
+    for (int b = 31; b >= 18; b--) {
+        const uint32_t c = T | (1u << b);
+        if (popc64(__ballot(hk >= c)) >= topK) T = c;
+    }
+    return T;
+}
+// One wave; lane l holds the logits of experts l + 64 j (j < 8). Writes the
+// topK entries of largest (logit key, lower ID) to s_ids[0, topK), ranked,
+// and returns true; returns false (s_ids untouched) when fewer than topK
+// lanes hold a valid entry or more than 64 entries pass the threshold (heavy
+// ties). `T0`, when not 0, is a threshold already found over a subset of
+// these logits (logit_threshold); with more than 64 entries at or above it,
+// the threshold of the complete set is searched and used instead.
+__device__ __forceinline__ bool select_by_logit(const float (&lg)[8], int experts, int topK, uint32_t T0,
+                                                RouterScratch &x, int *s_ids) {
+    const int lane = threadIdx.x & 63;
+    uint32_t k[8], hk = 0;
+    uint64_t Q[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        k[j] = lane + 64 * j < experts ? logit_key(lg[j]) : 0u;
+        hk = max(hk, k[j]);
+        Q[j] = ((uint64_t)k[j] << 9) | (uint64_t)(511 - (lane + 64 * j));
+    }
+    bool in[8];
+    if (T0 != 0u) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) in[j] = k[j] != 0u && k[j] >= T0;
+        if (rank_candidates(Q, in, topK, x, s_ids, false)) return true;
+    }
+    const uint32_t T = logit_threshold(hk, topK);
+    if (T == 0u) return false;
+#pragma unroll
+    for (int j = 0; j < 8; j++) in[j] = k[j] != 0u && k[j] >= T;
+    return rank_candidates(Q, in, topK, x, s_ids, false);
+}
+// One wave: the reference's probabilities for one token (kernels/strata.cu:
+// 243-254); lane l holds the logits of experts l + 64 j (-FLT_MAX past
+// `experts`). The maximum, the exponentials, the lane-strided sum (entries
+// past `experts` add +0, which changes nothing) and its tree, then
+// p = e * (1 / sum): q[j] in registers and in s.p[l + 64 j] (+0 past
+// `experts`). s_tab must already hold kExp2Tab.
+__device__ __forceinline__ void router_probs_wave(const float (&l)[8], int experts, const uint64_t *s_tab,
+                                                  RouterScratch &s, float (&q)[8]) {
+    const int lane = threadIdx.x & 63;
+    float mx = l[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) mx = fmaxf(mx, l[j]);
+    mx = wave_max(mx);
+    wave_lds_sync();  // this wave's copy of the exp table is in LDS
+    float d[8], e[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) d[j] = l[j] - mx;
+    expf_or_n<8>(d, e, s_tab);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        e[j] = lane + 64 * j < experts ? e[j] : 0.0f;
+        sum = sum + e[j];
+    }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, tree_sum64(sum))));
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        q[j] = e[j] * inv;
+        s.p[lane + 64 * j] = q[j];
+    }
+}
+// One wave, after router_probs_wave (q, and the same values in s.p). With
+// `spec`, s_ids[0, topK) holds select_by_logit's candidate c_0..c_{topK-1};
+// it is exactly the reference's selection when p(c_0) > p(c_1) > ... >
+// p(c_{topK-1}) and exactly topK entries have p >= p(c_{topK-1}): those topK
+// entries are then the candidate's (each of them has p >= p(c_{topK-1})),
+// every other entry has a smaller p (NaN never compares), and round k's
+// unique largest is c_k. Otherwise select_ranked overwrites s_ids. The
+// selected probabilities go to s.val[0, topK). Returns true when the
+// candidate stood.
+__device__ __forceinline__ bool router_confirm(const float (&q)[8], int experts, int topK, bool spec,
+                                               RouterScratch &s, int *s_ids) {
+    const int lane = threadIdx.x & 63;
+    bool stood = false;
+    if (spec) {
+        const float P = s.p[lane < topK ? s_ids[lane] : 0];
+        const float next = __builtin_bit_cast(
+            float, __builtin_amdgcn_ds_bpermute(((lane + 1) & 63) << 2, __builtin_bit_cast(int, P)));
+        const bool chain = lane >= topK - 1 || P > next;
+        const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, P), topK - 1));
+        int count = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) count += popc64(__ballot(lane + 64 * j < experts && q[j] >= last));
+        stood = __ballot(!chain) == 0 && count == topK;
+        if (stood && lane < topK) s.val[lane] = P;
+    }
+    if (!stood) {
+        int key[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) key[j] = select_key(q[j], lane + 64 * j < experts);
+        select_ranked(key, experts, topK, s, s_ids);
+    }
+    return stood;
 }
 
 }  // namespace sm

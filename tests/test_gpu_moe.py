@@ -195,6 +195,13 @@ def routing_styles(E):
     styles["pos_inf"][100] = np.inf
     styles["one_finite"] = np.full(E, -np.inf, np.float32)
     styles["one_finite"][7] = 0.0
+    # adjacent floats, the larger at the higher ID: their exponentials round
+    # to the same probability, so the reference takes the lower ID (smaller
+    # logit) first, against the logits' own order
+    u = (np.random.default_rng(11).normal(0, 1, E // 2) * 0.05).astype(np.float32)
+    styles["ulp_pairs"] = np.empty(E, np.float32)
+    styles["ulp_pairs"][0::2] = u
+    styles["ulp_pairs"][1::2] = np.nextafter(u, np.float32(np.inf))
     return styles
 
 
