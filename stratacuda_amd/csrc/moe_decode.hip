@@ -897,6 +897,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     __shared__ float s_parts[(kFusedMaxTopk + 2) * 8];
     __shared__ __attribute__((aligned(16))) float s_h[kFusedWaves][2][8 * DN_PITCH];
     __shared__ uint32_t s_arrive;
+    __shared__ float s_sig;
     __shared__ int s_ok, s_spec, s_reload, s_staged, s_selected, s_recs;
     __shared__ float s_logit[512];
 #ifdef SM_FUSED_TRACE
@@ -1121,19 +1122,6 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     if (wave == 1) {
         const bool stood = sm::router_confirm(prob, experts, topk, s_spec, s_router, s_ids);
         FUSED_MARK(4);
-        sm::wave_lds_sync();
-        // weights = selected / max(sum of selected, 2^-14), sum in k order
-        float denom = 0.0f;
-        for (int k = 0; k < topk; ++k) denom = denom + s_router.val[k];
-        denom = fmaxf(denom, 0.00006103515625f);
-        if (lane < topk) {
-            const float wk = s_router.val[lane] / denom;
-            s_w[lane] = wk;
-            if (b == 0) {
-                a.ids[lane] = s_ids[lane];
-                a.weights[lane] = wk;
-            }
-        }
         if (lane == 0) s_reload = !stood;
     }
     sm::lds_barrier();
@@ -1185,10 +1173,24 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         FUSED_MARK(13);
     }
 
-    // ---- phase B wait; then the block's 8 output rows.
+    // ---- phase B wait; then the block's 8 output rows. Wave 1 forms the
+    // routing weights meanwhile (only the combine uses them):
+    // weights = selected / max(sum of selected, 2^-14), sum in k order.
     if (wave == 0) {
         if (ok) ok = wait_go(fused_go(a.sync, b % kFusedGoCopies), launch, fault);
         FUSED_MARK(8);
+    } else if (wave == 1) {
+        float denom = 0.0f;
+        for (int k = 0; k < topk; ++k) denom = denom + s_router.val[k];
+        denom = fmaxf(denom, 0.00006103515625f);
+        if (lane < topk) {
+            const float wk = s_router.val[lane] / denom;
+            s_w[lane] = wk;
+            if (b == 0) {
+                a.ids[lane] = s_ids[lane];
+                a.weights[lane] = wk;
+            }
+        }
     }
     __syncthreads();
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
@@ -1204,7 +1206,11 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         hq[q][0] = load16_coherent(hr, off);
         hq[q][1] = load16_coherent(hr, off + 16);
     }
-    const float shared_gate = load_coherent(a.gate);
+    // the shared expert's gate, sigmoid(gate logit), by a wave with one slot
+    if (wave == kFusedWaves - 1) {
+        const float sig = sm::sigmoid(load_coherent(a.gate), s_tab);
+        if (lane == 0) s_sig = sig;
+    }
     // Read with the hidden rows rather than after the products: a wait that
     // gave up in any block set the fault word before that block's flag, so
     // before the go word; this block's own give-ups are in wave 0's `ok`
@@ -1278,8 +1284,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     __syncthreads();
     if (tid < 8) {
         const int r = b * 8 + tid;
-        const float sig = sm::sigmoid(shared_gate, s_tab);
-        float value = s_parts[topk * 8 + tid] * sig;
+        float value = s_parts[topk * 8 + tid] * s_sig;
         for (int k = 0; k < topk; k++) value = value + s_parts[k * 8 + tid] * s_w[k];
         if (faulted) value = __builtin_nanf("");
         a.Y[r] = NORM ? xres + value : value;
