@@ -829,6 +829,8 @@ __device__ bool collect(uint32_t *flags, uint32_t *sync, uint32_t launch, uint32
             return true;
         }
         __builtin_amdgcn_s_sleep(1);
+        // the flags change under this wave: no poll may reuse an earlier one's value
+        __asm__ volatile("" ::: "memory");
     }
     set_fault(fault);
     return false;
