@@ -54,6 +54,7 @@ extern "C" {
 #define SM_E_NOKERNEL (-5)   /* unknown kernel name (src/backend.js:103) */
 #define SM_E_ROUTE (-6)      /* invalid routing result detected on the device */
 #define SM_E_NOMEM (-7)      /* allocation failed */
+#define SM_E_FAULT (-8)      /* a device-side wait of the single-launch decode layer gave up (sm_fused_reset) */
 
 typedef struct sm_ctx sm_ctx;
 
@@ -64,6 +65,29 @@ const char *sm_last_error(sm_ctx *ctx);
 /* Writes a JSON object describing the device and counters (GpuBackend.info,
  * src/backend.js:120) into buf; returns the length or a negative code. */
 int sm_info(sm_ctx *ctx, char *buf, size_t cap);
+
+/* The single-launch decode layer (one token at hidden 2048 / ff 512; see
+ * sm_moe_layer) spreads one layer over 256 blocks that wait for each other,
+ * so it runs only when the device can hold all of them at once: sm_init
+ * checks the CU count against the kernel's occupancy (sm_info "fusedDecode";
+ * otherwise the three-kernel path runs). Every wait of the kernel is bounded:
+ * one that gives up (blocks not all resident, e.g. CUs held by another
+ * process) makes the layer's outputs NaN and sets a sticky fault, and so are
+ * the outputs of every later such launch on the context. sm_sync and sm_read
+ * then return SM_E_FAULT (the read still copies), as the reference rejects
+ * read / idle after a failed dispatch (src/backend.js:95,118); the
+ * reference's engine then marks the session failed (src/engine.js:195).
+ * sm_fused_reset waits for the context's work and clears the fault and the
+ * kernel's synchronisation words. sm_fused_fits(cus, blocks_per_cu) is the
+ * selection rule (1 when 256 blocks fit). sm_fused_test_hooks exists for
+ * tests of the give-up path only: spin_limit sets the polls before a wait
+ * gives up (0 = the default 2^20), withhold != 0 makes the kernel's collector
+ * wait for a flag no block writes, so the launch gives up with every kernel
+ * still ending normally. No reference counterpart (the reference's WebGPU
+ * and WASM kernels do not wait across workgroups). */
+int sm_fused_fits(int compute_units, int blocks_per_cu);
+int sm_fused_reset(sm_ctx *ctx);
+int sm_fused_test_hooks(sm_ctx *ctx, uint32_t spin_limit, int withhold);
 
 /* ---------------------------------------------------------------- buffers */
 /* zero != 0 clears the new buffer; refused (SM_E_ARG) while a graph is being

@@ -20,7 +20,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libstrata_mi355x.so")
 
 SM_OK = 0
-ERRORS = {-1: "hip", -2: "argument", -3: "bounds", -4: "handle", -5: "no kernel", -6: "route", -7: "memory"}
+ERRORS = {-1: "hip", -2: "argument", -3: "bounds", -4: "handle", -5: "no kernel", -6: "route", -7: "memory",
+          -8: "fused decode fault"}
+SM_E_FAULT = -8
 
 _TYPES = {"f32": np.float32, "i32": np.int32, "u32": np.uint32}
 _lib = None
@@ -83,6 +85,9 @@ def lib():
             "sm_synth_uniform_pm": (i, [vp, u64, u64, u64, u64, u64, ctypes.c_double]),
             "sm_synth_blobs": (i, [vp, u64, u64, u64, i, i, i, u64, u64, ctypes.c_double]),
             "sm_load_experts": (i, [vp, ctypes.c_char_p, u64, u64, i, u64, u64, u64, u64]),
+            "sm_fused_fits": (i, [i, i]),
+            "sm_fused_reset": (i, [vp]),
+            "sm_fused_test_hooks": (i, [vp, ctypes.c_uint32, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -213,6 +218,15 @@ class Backend:
 
     def idle(self):
         self._check(lib().sm_sync(self._ctx))
+
+    def fused_reset(self):
+        """Clears the single-launch decode layer's fault (sm_fused_reset)."""
+        self._check(lib().sm_fused_reset(self._ctx))
+
+    def fused_test_hooks(self, spin_limit=0, withhold=False):
+        """Test hook of the give-up path: poll limit (0 = default) and a collector
+        that waits for a flag no block writes (sm_fused_test_hooks)."""
+        self._check(lib().sm_fused_test_hooks(self._ctx, spin_limit, 1 if withhold else 0))
 
     sync = idle
 

@@ -29,6 +29,7 @@ const char *code_name(int rc) {
     case SM_E_NOKERNEL: return "SM_E_NOKERNEL";
     case SM_E_ROUTE: return "SM_E_ROUTE";
     case SM_E_NOMEM: return "SM_E_NOMEM";
+    case SM_E_FAULT: return "SM_E_FAULT";
     default: return "SM_E_UNKNOWN";
     }
 }
@@ -514,6 +515,15 @@ napi_value GraphFree(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// Clears the single-launch decode layer's fault (sm_fused_reset).
+napi_value FusedReset(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!a.need(1)) return nullptr;
+    sm_ctx *ctx = a.ctx(0);
+    if (!a.ok || fail(env, ctx, sm_fused_reset(ctx))) return nullptr;
+    return undefined(env);
+}
+
 napi_value ModuleInit(napi_env env, napi_value exports) {
     struct Fn {
         const char *name;
@@ -548,7 +558,8 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
                {"graphBegin", GraphBegin},
                {"graphEnd", GraphEnd},
                {"graphLaunch", GraphLaunch},
-               {"graphFree", GraphFree}};
+               {"graphFree", GraphFree},
+               {"fusedReset", FusedReset}};
     for (const Fn &f : fns) {
         napi_value fn;
         napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);

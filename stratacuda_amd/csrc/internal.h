@@ -51,6 +51,16 @@ struct sm_ctx {
     hipEvent_t staged[2] = {nullptr, nullptr};
     // Device address of this device's static decode scratch (sm_init).
     void *scratch = nullptr;
+    // The single-launch decode layer: enabled when all its blocks can be
+    // resident at once (sm_init); its poll limit and the test-only withhold
+    // switch (sm_fused_test_hooks); a pinned host word its kernels set when a
+    // wait gives up (read after every synchronisation, cleared by
+    // sm_fused_reset).
+    bool fused_capable = false;
+    uint32_t fused_spin_limit = 0, fused_withhold = 0;
+    uint32_t *fault_host = nullptr, *fault_dev = nullptr;  // host pointer, and its device address
+    // Captured graphs kept beside their executables until sm_graph_free.
+    std::vector<hipGraph_t> graph_sources;
 };
 
 namespace smi {
@@ -92,8 +102,15 @@ enum Stage {
 int stage_mark(sm_ctx *ctx, int stage);
 constexpr int kCounterWords = 16384;
 constexpr int kFusedSyncBase = 1024;
-// Index in ctx->counters of the fused decode layer's sticky fault word.
+// Index in ctx->counters of the fused decode layer's sticky fault word, and
+// the size in words of its synchronisation area (from kFusedSyncBase).
 uint32_t fused_fault_word();
+uint32_t fused_sync_words();
+// Whether kFusedBlocks blocks fit at once on `compute_units` CUs holding
+// `blocks_per_cu` blocks each; fused_decode_init sets ctx->fused_capable
+// from the device's CU count and the kernel's occupancy.
+bool fused_fits(int compute_units, int blocks_per_cu);
+int fused_decode_init(sm_ctx *ctx);
 inline bool stage_on(const sm_ctx *ctx, int stage) { return (ctx->stage_mask >> stage) & 1u; }
 // Zero-fills n 32-bit words with a kernel (graph-capturable, unlike a memset node).
 int zero_words(sm_ctx *ctx, void *dst, uint64_t n);

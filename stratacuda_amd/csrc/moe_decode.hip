@@ -729,8 +729,12 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
 // Plain stores and loads only: atomics on one address serialize (~14 ns
 // each on MI355X). The launch number is the go word's value when the block
 // starts plus one (the previous launch left it there), so nothing needs
-// resetting. Every wait gives up after kFusedSpinLimit
-// polls, setting a sticky fault word; the layer's outputs are then NaN.
+// resetting. Every wait gives up after kFusedSpinLimit polls (a launch
+// argument, so a test can lower it), setting a sticky fault word and its
+// host-visible mirror; the layer's outputs are then NaN, and so are those
+// of every later launch until sm_fused_reset. The kernel needs all
+// kFusedBlocks blocks resident at once: sm_init enables it only when the
+// device's CU count times its occupancy (one block per CU) covers them.
 constexpr int kFusedBlocks = 256, kFusedWaves = 8;
 constexpr int kFusedRows = 3;  // hidden rows per wave: ceil(11 x 512 / 2048)
 constexpr int kFusedWidth = 2048, kFusedFF = 512, kFusedMaxTopk = 10;
@@ -765,6 +769,13 @@ struct FusedArgs {
     uint32_t *sync;
     float eps;
     int experts, topk;
+    // Polls before a wait gives up (kFusedSpinLimit unless a test lowers it)
+    // and, for tests of the give-up path only, a non-zero `withhold`: the
+    // collector then waits for a flag value no block writes.
+    uint32_t spin_limit, withhold;
+    // Host-visible mirror of the fault word (pinned host memory): written
+    // only when a wait gives up, read by the host after a synchronisation.
+    uint32_t *fault_host;
 };
 
 __device__ __forceinline__ void store_coherent(float *p, float v) {
@@ -787,8 +798,13 @@ __device__ __forceinline__ void loads_ordered() {
     __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
-__device__ __forceinline__ void set_fault(uint32_t *fault) {
-    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_or(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Marks a give-up: the device fault word (read by later launches, which
+// then write NaN) and its host-visible mirror (read by sm_sync / sm_read).
+__device__ __forceinline__ void set_fault(uint32_t *fault, uint32_t *fault_host) {
+    if ((threadIdx.x & 63) == 0) {
+        __hip_atomic_fetch_or(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(fault_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 }
 // 16 coherent bytes at byte offset `off` of a buffer (buffer load with the sc1
 // policy: served from the coherence point, not a stale L2 line).
@@ -798,10 +814,10 @@ __device__ __forceinline__ float4 load16_coherent(__amdgpu_buffer_rsrc_t r, uint
     return make_float4(v.x, v.y, v.z, v.w);
 }
 // Whole-wave wait for the go word to reach `launch`. Returns false (and sets
-// the sticky fault word) after kFusedSpinLimit polls.
-__device__ bool wait_go(uint32_t *go, uint32_t launch, uint32_t *fault) {
+// the sticky fault word) after `limit` polls.
+__device__ bool wait_go(uint32_t *go, uint32_t launch, uint32_t limit, uint32_t *fault, uint32_t *fault_host) {
     const uint32_t want = (uint32_t)__builtin_amdgcn_readfirstlane((int)launch);
-    for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+    for (uint32_t i = 0; i < limit; i++) {
         const uint32_t v = (uint32_t)__builtin_amdgcn_readfirstlane((int)load_coherent_u32(go));
         if ((int)(v - want) >= 0) {
             loads_ordered();
@@ -809,31 +825,44 @@ __device__ bool wait_go(uint32_t *go, uint32_t launch, uint32_t *fault) {
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    set_fault(fault);
+    set_fault(fault, fault_host);
     return false;
 }
 // The collector: one wave reads the 256 flags of a phase (4 per lane) until
-// all hold `launch`, then publishes `launch` in every copy of the go word.
-__device__ bool collect(uint32_t *flags, uint32_t *sync, uint32_t launch, uint32_t *fault) {
-    const uint32_t want = (uint32_t)__builtin_amdgcn_readfirstlane((int)launch);
+// all hold `launch` (launch + withhold: a test's flag value that never comes),
+// then publishes `launch` in every copy of the go word. A collector that
+// gives up sets the fault word first and publishes the go word all the same:
+// the waiting blocks then see the fault at once (they read it after the go
+// word) instead of each spending its own poll limit, and the next launch
+// takes the number after this one, so no tag or flag this launch wrote can
+// pass as current there.
+__device__ bool collect(uint32_t *flags, uint32_t *sync, uint32_t launch, uint32_t limit, uint32_t withhold,
+                        uint32_t *fault, uint32_t *fault_host) {
+    const uint32_t want = (uint32_t)__builtin_amdgcn_readfirstlane((int)(launch + withhold));
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(flags, (short)0, kFusedBlocks * 4, 0x00020000);
     const uint32_t off = (uint32_t)(threadIdx.x & 63) * 16;
-    for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+    const uint32_t go = (uint32_t)__builtin_amdgcn_readfirstlane((int)launch);
+    bool all = false;
+    for (uint32_t i = 0; i < limit; i++) {
         const uint4 f = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16));
         const bool in = (int)(f.x - want) >= 0 && (int)(f.y - want) >= 0 && (int)(f.z - want) >= 0 &&
                         (int)(f.w - want) >= 0;
         if (__ballot(!in) == 0) {
             loads_ordered();
-            for (int c = threadIdx.x & 63; c < kFusedGoCopies; c += 64)
-                __hip_atomic_store(fused_go(sync, c), want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return true;
+            all = true;
+            break;
         }
         __builtin_amdgcn_s_sleep(1);
         // the flags change under this wave: no poll may reuse an earlier one's value
         __asm__ volatile("" ::: "memory");
     }
-    set_fault(fault);
-    return false;
+    if (!all) {
+        set_fault(fault, fault_host);
+        stores_complete();  // the fault word before the go word
+    }
+    for (int c = threadIdx.x & 63; c < kFusedGoCopies; c += 64)
+        __hip_atomic_store(fused_go(sync, c), go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return all;
 }
 // Records in LDS sit kRecPitch words apart: 16 bytes more than a record, so
 // the 16-byte reads of lanes reading different groups fall in different
@@ -1035,7 +1064,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         poll(t);
         bool all = false;
         uint32_t T0 = 0;
-        for (uint32_t i = 0; i < kFusedSpinLimit; i++) {
+        for (uint32_t i = 0; i < a.spin_limit; i++) {
             bool mine = true;
 #pragma unroll
             for (int j = 0; j < 8; j++) mine = mine && (uint32_t)(t[j] >> 32) == launch;
@@ -1056,7 +1085,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
 #pragma unroll
             for (int j = 0; j < 8; j++) t[j] = tn[j];
         }
-        if (!all) set_fault(fault);
+        if (!all) set_fault(fault, a.fault_host);
         ok = all;
         float lg[8];
 #pragma unroll
@@ -1176,8 +1205,11 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         dc[q] = load_codes(blob + a.down_codes + (uint64_t)drow * (kFusedFF / 4) + g8 * 16);
         dsb[q] = *(const uint16_t *)(blob + a.down_scales + ((uint64_t)drow * GD + g8) * 2);
     }
-    if (b == kFusedCollector && wave == kFusedWaves - 1 && ok) {
-        collect(a.sync + kFusedFlagsB, a.sync, launch, fault);
+    // The collector runs whatever its own block's state: every block writes
+    // its flag (a block that gave up included), and only the collector
+    // advances the go word.
+    if (b == kFusedCollector && wave == kFusedWaves - 1) {
+        collect(a.sync + kFusedFlagsB, a.sync, launch, a.spin_limit, a.withhold, fault, a.fault_host);
         FUSED_MARK(13);
     }
 
@@ -1185,7 +1217,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     // routing weights meanwhile (only the combine uses them):
     // weights = selected / max(sum of selected, 2^-14), sum in k order.
     if (wave == 0) {
-        if (ok) ok = wait_go(fused_go(a.sync, b % kFusedGoCopies), launch, fault);
+        if (ok) ok = wait_go(fused_go(a.sync, b % kFusedGoCopies), launch, a.spin_limit, fault, a.fault_host);
         FUSED_MARK(8);
     } else if (wave == 1) {
         float denom = 0.0f;
@@ -1350,6 +1382,29 @@ int static_scratch_init(sm_ctx *ctx) {
 }
 
 uint32_t fused_fault_word() { return kFusedSyncBase + kFusedFaultWord; }
+uint32_t fused_sync_words() { return kFusedSyncWords; }
+
+bool fused_fits(int compute_units, int blocks_per_cu) {
+    return compute_units > 0 && blocks_per_cu > 0 && (int64_t)compute_units * blocks_per_cu >= kFusedBlocks;
+}
+
+int fused_decode_init(sm_ctx *ctx) {
+    // Both instantiations have the same resources; the one-block-per-CU
+    // bound makes this 0 or 1 on a CDNA CU.
+    int per_cu = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_fused<true>, 64 * kFusedWaves, 0);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipOccupancyMaxActiveBlocksPerMultiprocessor(k_decode_fused)");
+    int per_cu2 = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, k_decode_fused<false>, 64 * kFusedWaves, 0);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipOccupancyMaxActiveBlocksPerMultiprocessor(k_decode_fused)");
+    int cus = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipDeviceGetAttribute(multiProcessorCount)");
+    ctx->fused_capable = fused_fits(cus, per_cu < per_cu2 ? per_cu : per_cu2);
+    ctx->fused_spin_limit = kFusedSpinLimit;
+    ctx->fused_withhold = 0;
+    return SM_OK;
+}
 static_assert(kFusedSyncBase + kFusedSyncWords <= kCounterWords, "fused decode sync area");
 static_assert((kFusedSyncBase + kFusedLogitWords) % 2 == 0, "tagged logits are 8-byte words");
 
@@ -1385,8 +1440,9 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
     uint32_t *xq = (uint32_t *)(ws + w.xq);
     // One token at hidden 2048 / ff 512: the whole layer in one launch.
     const uint32_t decode_stages = (1u << kStageDecodeRoute) | (1u << kStageDecodeGateUp) | (1u << kStageDecodeDown);
-    if (tokens == 1 && width == kFusedWidth && ff == kFusedFF && experts <= 2 * kFusedBlocks && topk <= kFusedMaxTopk &&
-        stage_on(ctx, kStageDecodeFused) && (ctx->stage_mask & decode_stages) == decode_stages) {
+    if (ctx->fused_capable && tokens == 1 && width == kFusedWidth && ff == kFusedFF && experts <= 2 * kFusedBlocks &&
+        topk <= kFusedMaxTopk && stage_on(ctx, kStageDecodeFused) &&
+        (ctx->stage_mask & decode_stages) == decode_stages) {
         if (int rc = stage_mark(ctx, kStageDecodeFused)) return rc;
         FusedArgs fa;
         fa.X = (const float *)X;
@@ -1410,6 +1466,9 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
         fa.eps = eps;
         fa.experts = experts;
         fa.topk = topk;
+        fa.spin_limit = ctx->fused_spin_limit;
+        fa.withhold = ctx->fused_withhold;
+        fa.fault_host = ctx->fault_dev;
         const auto kf = gamma ? k_decode_fused<true> : k_decode_fused<false>;
         kf<<<kFusedBlocks, 64 * kFusedWaves, 0, ctx->stream>>>(fa);
         if (int rc = launched(ctx)) return rc;

@@ -1120,12 +1120,18 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         return rc;
     }
 
-    if (int rc2 = stage_mark(ctx, kStagePrefillRoute)) return rc2;
+    // From here on the second stream holds work: every early return joins
+    // it first, so a capture stays valid and no aux kernel outlives the call.
+    auto bail = [ctx](int code) {
+        (void)join_aux(ctx);
+        return code;
+    };
+    if (int rc2 = stage_mark(ctx, kStagePrefillRoute)) return bail(rc2);
     if (int rc2 = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts,
                                topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
                                (float *)(ws + w.gate)))
-        return rc2;
-    if (int rc2 = stage_mark(ctx, kStagePrefillDispatch)) return rc2;
+        return bail(rc2);
+    if (int rc2 = stage_mark(ctx, kStagePrefillDispatch)) return bail(rc2);
     int *offsets = (int *)(ws + w.offsets);
     int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);
     const int4 *info_small = (const int4 *)(ws + w.info_small), *info_big = (const int4 *)(ws + w.info_big);
@@ -1137,8 +1143,8 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     if (int rc2 = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
                                   (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch,
                                   shared_first ? 0 : 1, &tiling))
-        return rc2;
-    if (int rc2 = wait_aux_mark(ctx)) return rc2;
+        return bail(rc2);
+    if (int rc2 = wait_aux_mark(ctx)) return bail(rc2);
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const uint64_t segs = (uint64_t)experts + 1;
     // Segment tilings: `split` or more rows in 64-row tiles ("big"), fewer in
@@ -1192,10 +1198,10 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         }
         return launched(ctx);
     };
-    if (int rc2 = stage_mark(ctx, kStagePrefillGateUp)) return rc2;
-    if (int rc2 = gemms(true, xhl, rows, width, 2 * ff, L.gate_up_codes, L.gate_up_scales, ws + w.Hhl, ff)) return rc2;
-    if (int rc2 = stage_mark(ctx, kStagePrefillDown)) return rc2;
-    if (int rc2 = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return rc2;
+    if (int rc2 = stage_mark(ctx, kStagePrefillGateUp)) return bail(rc2);
+    if (int rc2 = gemms(true, xhl, rows, width, 2 * ff, L.gate_up_codes, L.gate_up_scales, ws + w.Hhl, ff)) return bail(rc2);
+    if (int rc2 = stage_mark(ctx, kStagePrefillDown)) return bail(rc2);
+    if (int rc2 = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return bail(rc2);
     // Everything on the second stream (the shared expert's products) is in
     // before the combine reads P.
     if (int rc2 = join_aux(ctx)) return rc2;

@@ -139,6 +139,19 @@ int sm_init(int device, sm_ctx **out) {
         sm_shutdown(ctx);
         return SM_E_HIP;
     }
+    // The fused decode layer's host-visible fault word: coherent pinned host
+    // memory, so a kernel's store reaches it without a copy.
+    if (hipHostMalloc((void **)&ctx->fault_host, 64, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) {
+        ctx->fault_host = nullptr;
+        sm_shutdown(ctx);
+        return SM_E_HIP;
+    }
+    *(volatile uint32_t *)ctx->fault_host = 0;
+    if (hipHostGetDevicePointer((void **)&ctx->fault_dev, ctx->fault_host, 0) != hipSuccess || !ctx->fault_dev ||
+        fused_decode_init(ctx) != SM_OK) {
+        sm_shutdown(ctx);
+        return SM_E_HIP;
+    }
     *out = ctx;
     return SM_OK;
 }
@@ -155,6 +168,9 @@ void sm_shutdown(sm_ctx *ctx) {
     for (auto &e : ctx->stage_pool) (void)hipEventDestroy(e);
     for (auto &g : ctx->graphs)
         if (g) (void)hipGraphExecDestroy(g);
+    for (auto &g : ctx->graph_sources)
+        if (g) (void)hipGraphDestroy(g);
+    if (ctx->fault_host) (void)hipHostFree(ctx->fault_host);
     for (auto &e : ctx->events)
         if (e) (void)hipEventDestroy(e);
     if (ctx->fork) (void)hipEventDestroy(ctx->fork);
@@ -172,22 +188,49 @@ int sm_info(sm_ctx *ctx, char *buf, size_t cap) {
     hipDeviceProp_t p;
     HIP_TRY(ctx, hipGetDeviceProperties(&p, ctx->device));
     // The fused decode layer's sticky fault word (a wait that gave up); read
-    // synchronously, so only outside a capture (-1 while capturing).
+    // after a synchronisation, so only outside a capture (-1 while capturing).
     long long faults = -1;
     if (!ctx->capturing) {
         uint32_t f = 0;
         HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
         HIP_TRY(ctx, hipMemcpy(&f, ctx->counters + fused_fault_word(), sizeof(f), hipMemcpyDeviceToHost));
-        faults = f;
+        faults = f | *(volatile uint32_t *)ctx->fault_host;
     }
     int n = snprintf(buf, cap,
                      "{\"backend\":\"hip\",\"device\":%d,\"name\":\"%s\",\"arch\":\"%s\",\"computeUnits\":%d,"
                      "\"globalMemoryBytes\":%llu,\"dispatches\":%llu,\"allocatedBytes\":%llu,\"buffers\":%zu,"
-                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu,\"fusedDecodeFault\":%lld}",
+                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu,\"fusedDecode\":%s,\"fusedDecodeFault\":%lld}",
                      ctx->device, p.name, p.gcnArchName, p.multiProcessorCount, (unsigned long long)p.totalGlobalMem,
                      (unsigned long long)ctx->launches, (unsigned long long)ctx->allocated, ctx->buffers.size(),
-                     (unsigned long long)ctx->bytes_written, (unsigned long long)ctx->bytes_read, faults);
+                     (unsigned long long)ctx->bytes_written, (unsigned long long)ctx->bytes_read,
+                     ctx->fused_capable ? "true" : "false", faults);
     return n;
+}
+
+int sm_fused_fits(int compute_units, int blocks_per_cu) { return fused_fits(compute_units, blocks_per_cu) ? 1 : 0; }
+
+int sm_fused_reset(sm_ctx *ctx) {
+    if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
+    if (!ctx) return SM_E_ARG;
+    // Every queued launch has ended (each wait is bounded) before the
+    // synchronisation area is cleared: go words, flags and tags back to 0
+    // (the next launch is number 1, which nothing left behind carries), and
+    // the fault word with its host mirror.
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->aux));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemsetAsync(ctx->counters + kFusedSyncBase, 0, (size_t)fused_sync_words() * sizeof(uint32_t),
+                                ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    *(volatile uint32_t *)ctx->fault_host = 0;
+    return SM_OK;
+}
+
+int sm_fused_test_hooks(sm_ctx *ctx, uint32_t spin_limit, int withhold) {
+    if (!ctx) return SM_E_ARG;
+    if (ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
+    ctx->fused_spin_limit = spin_limit ? spin_limit : (1u << 20);
+    ctx->fused_withhold = withhold ? 1u : 0u;
+    return SM_OK;
 }
 
 int sm_alloc(sm_ctx *ctx, uint64_t bytes, int zero, uint64_t *handle) {
@@ -243,6 +286,17 @@ int sm_write(sm_ctx *ctx, uint64_t dst, uint64_t dst_offset, const void *src, ui
     return SM_OK;
 }
 
+// After a synchronisation: SM_E_FAULT when a wait of the single-launch
+// decode layer gave up (its outputs, and those of every later launch until
+// sm_fused_reset, are NaN).
+static int fused_fault_check(sm_ctx *ctx) {
+    if (ctx->fault_host && *(volatile uint32_t *)ctx->fault_host)
+        return fail(ctx, SM_E_FAULT,
+                    "the single-launch decode layer gave up waiting for other blocks (not all of them resident); "
+                    "its outputs are NaN until sm_fused_reset");
+    return SM_OK;
+}
+
 int sm_read(sm_ctx *ctx, uint64_t src, uint64_t src_offset, void *dst, uint64_t bytes) {
     if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     if (!ctx || (!dst && bytes)) return SM_E_ARG;
@@ -250,7 +304,7 @@ int sm_read(sm_ctx *ctx, uint64_t src, uint64_t src_offset, void *dst, uint64_t 
     if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, (const char *)src + src_offset, bytes, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     ctx->bytes_read += bytes;
-    return SM_OK;
+    return fused_fault_check(ctx);
 }
 
 int sm_copy(sm_ctx *ctx, uint64_t src, uint64_t src_offset, uint64_t dst, uint64_t dst_offset, uint64_t bytes) {
@@ -282,7 +336,7 @@ int sm_sync(sm_ctx *ctx) {
     if (ctx && ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     if (!ctx) return SM_E_ARG;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    return SM_OK;
+    return fused_fault_check(ctx);
 }
 
 int sm_stage_timing(sm_ctx *ctx, int enable) {
@@ -335,9 +389,15 @@ int sm_graph_end(sm_ctx *ctx, int *graph_id) {
     HIP_TRY(ctx, hipStreamEndCapture(ctx->stream, &graph));
     hipGraphExec_t exec = nullptr;
     hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return hip_fail(ctx, e, "hipGraphInstantiate");
+    }
+    // The captured graph is kept until sm_graph_free, beside its executable:
+    // a tool that maps an executable's nodes back to their source graph then
+    // finds it alive.
     ctx->graphs.push_back(exec);
+    ctx->graph_sources.push_back(graph);
     *graph_id = (int)ctx->graphs.size() - 1;
     return SM_OK;
 }
@@ -353,6 +413,8 @@ int sm_graph_free(sm_ctx *ctx, int graph_id) {
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     HIP_TRY(ctx, hipGraphExecDestroy(ctx->graphs[graph_id]));
     ctx->graphs[graph_id] = nullptr;
+    if (ctx->graph_sources[graph_id]) HIP_TRY(ctx, hipGraphDestroy(ctx->graph_sources[graph_id]));
+    ctx->graph_sources[graph_id] = nullptr;
     return SM_OK;
 }
 

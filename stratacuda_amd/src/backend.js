@@ -170,7 +170,21 @@ export class HipBackend {
         const id = this.owned(buffer, 'read');
         this.assertAlive();
         if (!typed[type]) throw Error('Unsupported buffer type ' + type);
-        return new typed[type](this.addon.read(this.ctx, id, 0, buffer.byteLength));
+        let bytes;
+        try { bytes = this.addon.read(this.ctx, id, 0, buffer.byteLength); } catch (error) {
+            // a wait of the single-launch decode layer gave up: the backend
+            // fails like a lost device until resetFusedDecode()
+            if (error.code === 'SM_E_FAULT') this.failure = error;
+            throw error;
+        }
+        return new typed[type](bytes);
+    }
+    // Clears the single-launch decode layer's fault (after SM_E_FAULT from
+    // read() or idle()); later launches compute again.
+    resetFusedDecode() {
+        if (!this.ctx) throw Error('HIP backend is disposed');
+        this.addon.fusedReset(this.ctx);
+        if (this.failure && this.failure.code === 'SM_E_FAULT') this.failure = null;
     }
     // Bytes [offset, offset + bytes) of a buffer as an ArrayBuffer.
     async readBytes(buffer, offset, bytes) {

@@ -24,7 +24,7 @@ test('the addon exports every entry of the C ABI it wraps', () => {
         'sync', 'kernels', 'signature', 'run', 'moeWorkspace', 'moeLayer', 'moeBlockWorkspace', 'moeBlock', 'moeRoute',
         'moeDispatch', 'synthNormal',
         'synthUniformPm', 'synthBlobs', 'eventRecord', 'eventElapsed', 'graphBegin', 'graphEnd', 'graphLaunch',
-        'graphFree'])
+        'graphFree', 'fusedReset'])
         assert.strictEqual(typeof real[f], 'function', f);
     assert.ok(real.kernels().indexOf('strata_router') >= 0);
     assert.strictEqual(real.signature('strata_router'), 'Logits:f32*,Ids:i32*,Weights:f32*,experts:i32,topK:i32');
@@ -188,6 +188,28 @@ test('moeBlock passes the layer gamma and the resident buffers in the C ABI orde
     assert.deepStrictEqual(call.args.slice(14, 17), [r.h.id, r.ids.id, r.weights.id]);
     assert.ok(call.args[18] >= real.moeBlockWorkspace(2, 128, 64, 16, 4));
     await assert.rejects(ops.moeBlock(0, h, 3), /MoE input must hold tokens x width values/);
+});
+
+test('a fused decode fault fails read() and idle() until resetFusedDecode()', async () => {
+    // SM_E_FAULT from the library (a device-side wait that gave up) rejects
+    // read and idle, as the reference rejects them after a failed dispatch
+    // (src/backend.js:95,118); the backend then fails every call like a lost
+    // device until the fault is cleared.
+    const addon = fakeAddon();
+    let faulted = true, resets = 0;
+    const fault = () => { const e = Error('the single-launch decode layer gave up'); e.code = 'SM_E_FAULT'; return e; };
+    const read = addon.read;
+    addon.read = (...a) => { if (faulted) throw fault(); return read(...a); };
+    addon.sync = () => { if (faulted) throw fault(); };
+    addon.fusedReset = () => { resets++; faulted = false; };
+    const b = await HipBackend.create({addon});
+    const y = b.alloc(new Float32Array([1, 2]));
+    await assert.rejects(b.read(y), {code: 'SM_E_FAULT'});
+    assert.throws(() => b.alloc(4), {code: 'SM_E_FAULT'});
+    b.resetFusedDecode();
+    assert.strictEqual(resets, 1);
+    assert.deepStrictEqual(Array.from(await b.read(y)), [1, 2]);
+    await b.idle();
 });
 
 run();

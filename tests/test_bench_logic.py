@@ -91,3 +91,34 @@ def test_gpus_other_than_one_exit_with_a_message(capsys, monkeypatch):
         bench.main()
     assert e.value.code == 2
     assert "one GPU" in capsys.readouterr().err
+
+
+def test_profiler_detection():
+    assert bench.under_profiler({"LD_PRELOAD": "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so"})
+    assert bench.under_profiler({"ROCPROF_KERNEL_TRACE": "1"})
+    assert not bench.under_profiler({"LD_PRELOAD": "", "PATH": "/usr/bin"})
+
+
+def test_graph_replays_refused_under_profiler(capsys, monkeypatch):
+    # Graph-replayed runs are not profiled (the profiler crashed inside
+    # hipGraphLaunch on them); --eager issues the same steps directly.
+    monkeypatch.setattr("sys.argv", ["bench.py", "--steps", "4"])
+    monkeypatch.setenv("ROCPROF_KERNEL_TRACE", "1")
+    with pytest.raises(SystemExit) as e:
+        bench.main()
+    assert e.value.code == 2
+    assert "--eager" in capsys.readouterr().err
+
+
+def test_flat_prefill_is_scalars_only():
+    r = {"tokens_per_s": 1.75e6, "ms_per_layer": 0.2925, "distinct_experts": 512,
+         "stage_us": {"prefill_route": 60.0, "prefill_dispatch": 24.0, "prefill_gate_up_gemm": 135.0,
+                      "prefill_down_gemm": 78.0, "prefill_combine": 14.0},
+         "hbm": {"bytes": 466460672, "achieved_GBs": 1594.7, "frac": 0.1993},
+         "mfma": {"layer_flops": 36.5e9, "layer_frac": 0.05}}
+    f = bench.flat_prefill("T=512", r, 2048, 512, 512, 10)
+    assert all(not isinstance(v, (dict, list)) for v in f.values())
+    assert f["roofline_bound"] == "hbm" and f["roofline_frac"] == 0.1993 and f["route_us"] == 60.0
+    z = bench.flat_prefill("T=2048 zipf", dict(r, ms_per_layer=0.5), 2048, 512, 512, 10)
+    assert z["roofline_bound"] == "mfma" and z["roofline_unit"] == "TFLOP/s"
+    assert abs(z["roofline_achieved"] - 36.5e9 / 0.5e-3 / 1e12) < 0.1

@@ -1,11 +1,17 @@
 """The single-launch decode layer (one token, hidden 2048 / ff 512) against
 the three-kernel decode path and the CPU oracle: the same bits as the three
 kernels (both compute every product and sum in the same order), routing
-bit-exact with the oracle, and the hand-off counters back at zero after
-every launch (many launches in a row, across layers, from a graph)."""
+bit-exact with the oracle, and no wait ever giving up (fusedDecodeFault 0)
+over many launches in a row, across layers and replayed from a graph: each
+launch takes the number after the go word the previous one left, so no
+counter is reset between launches. The give-up path is forced from the host
+(a low poll limit and a collector waiting for a flag no block writes, so
+every kernel still ends normally): NaN outputs, SM_E_FAULT from sync and
+read, the fault sticky until sm_fused_reset, bit-exact results after it."""
 import numpy as np
 import pytest
 
+import stratacuda_amd as sm
 from conftest import tol_ok
 from stratacuda_amd import workload as wl
 
@@ -165,3 +171,46 @@ def test_fused_stage_timing(backend, two_layers):
     b.stage_timing(False)
     assert rep["decode_fused"][1] == 4
     assert rep["decode_route"][1] == 0
+
+
+def test_fused_give_up_reported_and_reset(backend, two_layers):
+    b = backend
+    W, F, E, K = wl.WIDTH, wl.FF, wl.EXPERTS, wl.TOPK
+    assert b.info()["fusedDecode"] is True  # 256 CUs on an MI355X, one block each
+    lay = two_layers[0]
+    X = b.alloc(W, zero=False)
+    b.synth_normal(X, W, 31, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, W, F, E, K))
+    ids, w = b.alloc(K, "i32"), b.alloc(K)
+    Y0, Y1, Y2, Y3 = (b.alloc(W) for _ in range(4))
+    run_layer(b, lay, X, Y0, ids, w, ws, ALL)
+    y0 = b.read(Y0)
+    assert np.all(np.isfinite(y0))
+    try:
+        b.fused_test_hooks(spin_limit=64, withhold=True)
+        print("fused give-up: withheld launch", flush=True)
+        run_layer(b, lay, X, Y1, ids, w, ws, ALL)
+        with pytest.raises(sm.StrataError) as err:
+            b.idle()
+        assert err.value.code == sm.SM_E_FAULT
+        with pytest.raises(sm.StrataError) as err:
+            b.read(Y1)
+        assert err.value.code == sm.SM_E_FAULT
+        b.fused_test_hooks()
+        # sticky: a launch with every wait satisfied still writes NaN
+        run_layer(b, lay, X, Y2, ids, w, ws, ALL)
+        with pytest.raises(sm.StrataError):
+            b.idle()
+        assert b.info()["fusedDecodeFault"] == 1
+    finally:
+        b.fused_test_hooks()
+        b.fused_reset()
+    assert b.info()["fusedDecodeFault"] == 0
+    assert np.all(np.isnan(b.read(Y1))) and np.all(np.isnan(b.read(Y2)))
+    print("fused give-up: launch after reset", flush=True)
+    run_layer(b, lay, X, Y3, ids, w, ws, ALL)
+    assert np.array_equal(bits(b.read(Y3)), bits(y0))
+    # and again, from the three kernels' side: the same bits
+    run_layer(b, lay, X, Y1, ids, w, ws, THREE_KERNELS)
+    assert np.array_equal(bits(b.read(Y1)), bits(y0))
+    assert b.info()["fusedDecodeFault"] == 0

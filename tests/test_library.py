@@ -33,6 +33,19 @@ def test_library_exports_every_declared_symbol():
         getattr(lib, f)
 
 
+def test_fused_decode_selection_rule():
+    # The single-launch decode layer needs 256 blocks resident at once, one
+    # per CU: a whole MI355X (256 CUs) qualifies; its DPX / CPX partitions
+    # (128 / 32 CUs per partition), fewer CUs or no occupancy do not.
+    import stratacuda_amd as sm
+    L = sm.lib()
+    assert L.sm_fused_fits(256, 1) == 1
+    assert L.sm_fused_fits(304, 1) == 1
+    assert L.sm_fused_fits(128, 2) == 1
+    for cus, per_cu in [(255, 1), (128, 1), (32, 1), (256, 0), (0, 4), (-1, 1)]:
+        assert L.sm_fused_fits(cus, per_cu) == 0, (cus, per_cu)
+
+
 def test_library_contains_gfx950_code_object():
     import stratacuda_amd as sm
     data = open(sm.LIB_PATH, "rb").read()
