@@ -178,6 +178,21 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
                  int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,
                  uint64_t workspace_bytes);
 
+/* Diagnostics of the batch router (no reference counterpart). For 512 or
+ * more tokens sm_moe_layer / sm_moe_block route with a certified router: every
+ * logit approximately on fp16 MFMA with a worst-case error bound, then the
+ * exact reference-order logits of the experts near each token's top-k
+ * boundary only; a token whose order the bound cannot certify (ties within
+ * rounding, underflow, NaN or inf, more than 64 candidates) takes every
+ * logit exactly. IDs and their order are the reference's either way; the
+ * routing weights agree with the reference's to a few ulp. After such a
+ * call (synchronously) this reads the workspace's per-token records:
+ * candidates = exact logits formed over all tokens, fallbacks = tokens that
+ * took the exact path. Returns the number of tokens covered, 0 when the
+ * batch did not use the certified router, or a negative code. */
+int sm_moe_route_stats(sm_ctx *ctx, uint64_t workspace, int tokens, int width, int ff, int experts, int topk,
+                       uint64_t *candidates, int *fallbacks);
+
 /* Allocation-free variant of sm_moe_layer for the decode path (no reference
  * counterpart: it is for callers that cannot allocate, such as code under
  * HIP graph capture or a serving loop that forbids hipMalloc). Same

@@ -86,6 +86,7 @@ def lib():
             "sm_synth_blobs": (i, [vp, u64, u64, u64, i, i, i, u64, u64, ctypes.c_double]),
             "sm_load_experts": (i, [vp, ctypes.c_char_p, u64, u64, i, u64, u64, u64, u64]),
             "sm_fused_fits": (i, [i, i]),
+            "sm_moe_route_stats": (i, [vp, u64, i, i, i, i, i, pu64, ctypes.POINTER(i)]),
             "sm_fused_reset": (i, [vp]),
             "sm_fused_test_hooks": (i, [vp, ctypes.c_uint32, i]),
         }
@@ -218,6 +219,16 @@ class Backend:
 
     def idle(self):
         self._check(lib().sm_sync(self._ctx))
+
+    def route_stats(self, workspace, tokens, width, ff, experts, topk):
+        """(candidates, fallbacks) of the certified batch router's last call on
+        this workspace, or None when the batch did not use it."""
+        c, f = ctypes.c_uint64(0), ctypes.c_int(0)
+        n = lib().sm_moe_route_stats(self._ctx, workspace.handle, tokens, width, ff, experts, topk, ctypes.byref(c),
+                                     ctypes.byref(f))
+        if n < 0:
+            self._check(n)
+        return (int(c.value), int(f.value)) if n > 0 else None
 
     def fused_reset(self):
         """Clears the single-launch decode layer's fault (sm_fused_reset)."""

@@ -21,7 +21,7 @@ ADDON = os.path.join(HERE, "src", "strata_addon.node")
 OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["kernels_ref.hip", "kernels_model.hip", "moe_route.hip", "moe_decode.hip", "moe_prefill.hip", "synth.hip", "pack_loader.hip"]
+HIP_SOURCES = ["kernels_ref.hip", "kernels_model.hip", "moe_route.hip", "moe_route_cert.hip", "moe_decode.hip", "moe_prefill.hip", "synth.hip", "pack_loader.hip"]
 HOST_SOURCES = ["runtime.cpp"]
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-Wall",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -121,6 +121,26 @@ int route(sm_ctx *ctx, uint64_t X, int tokens, int width, uint64_t Wr, uint64_t 
 // Unchecked launchers on raw device pointers (callers validated the buffers).
 int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float *Wr, const float *bias, int experts,
                  int topk, float *logits, int *ids, float *weights, const float *gate_w, float *gate_out);
+// The certified batch router (moe_route_cert.hip): approximate logits on
+// fp16 MFMA, exact reference-order logits for the candidates near the top-k
+// boundary only, per-token certification with an exact fallback. IDs and
+// their order bit-exact, weights within a few ulp. route_cert_prepare
+// converts W_r (fp16, the split activations' K order) into the workspace;
+// route_cert_launch then needs the fp16 hi/lo split of X (k_split_hilo's
+// layout). Per-token stats (uint32 candidates | 1 << 16 on a fallback) at
+// route_cert_stats_offset.
+// From 512 tokens on (graph replays of 8 layers on one MI355X, hidden 2048,
+// 512 experts, top-10: 384 tokens 253.5 us per layer certified against 253.1
+// exact, 512 tokens 265.4 against 266.2, 1024 tokens 379.5 against 397.2;
+// below 384 the exact router is 1-15 us faster).
+constexpr int kRouteCertMinTokens = 512;
+bool route_cert_applies(int tokens, int width, int experts, int topk);
+uint64_t route_cert_workspace(int tokens, int width, int experts);
+uint64_t route_cert_stats_offset(int tokens, int width, int experts);
+int route_cert_prepare(sm_ctx *ctx, const float *Wr, int tokens, int width, int experts, char *ws);
+int route_cert_launch(sm_ctx *ctx, const float *X, const _Float16 *Xhl, int tokens, int width, const float *Wr,
+                      const float *bias, int experts, int topk, int *ids, float *weights, const float *gate_w,
+                      float *gate_out, char *ws);
 // M-tile bases the dispatch writes for the grouped GEMMs: segments with at
 // least `split` rows in tiles of mt_big rows (big[]), the others in tiles of
 // mt_small rows (small[]); each array has experts + 2 entries. When set,
@@ -169,6 +189,9 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                 uint64_t workspace_bytes, const BlockArgs *block = nullptr);
 // With block != nullptr the workspace also holds the normalised input.
 uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk, bool block = false);
+// Byte offset in a prefill workspace of the certified router's per-token
+// stats (uint32 each), -1 when the batch does not use that router.
+int64_t moe_prefill_route_stats_offset(int tokens, int width, int ff, int experts, int topk);
 // strata_norm mode 0 (scale 1) over `rows` rows of `cols`, on the context's stream.
 int norm_launch(sm_ctx *ctx, const float *X, const float *gamma, float *Y, int cols, int rows, float eps);
 

@@ -979,14 +979,15 @@ inline uint64_t big_tile_bound(uint64_t m, int experts) {
 }
 
 struct PrefillWs {
-    uint64_t logits, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, tiles_shared, info_shared,
+    uint64_t logits, rcert, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, tiles_shared, info_shared,
         rows, parts, where_, Xhl, Hhl, P, Xn, end;
 };
 PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool block = false) {
     const uint64_t n = (uint64_t)tokens * topk, m = n + tokens;
     PrefillWs w;
     w.logits = 0;
-    w.gate = up(w.logits + (uint64_t)tokens * experts * 4);
+    w.rcert = up(w.logits + (uint64_t)tokens * experts * 4);
+    w.gate = up(w.rcert + route_cert_workspace(tokens, width, experts));
     w.dispatch = up(w.gate + (uint64_t)tokens * 4);
     w.offsets = up(w.dispatch + dispatch_workspace(tokens, experts));
     w.tiles_small = up(w.offsets + ((uint64_t)experts + 2) * 4);
@@ -1012,6 +1013,12 @@ namespace smi {
 
 uint64_t moe_prefill_workspace(int tokens, int width, int ff, int experts, int topk, bool block) {
     return prefill_ws(tokens, width, ff, experts, topk, block).end;
+}
+
+int64_t moe_prefill_route_stats_offset(int tokens, int width, int ff, int experts, int topk) {
+    if (!route_cert_applies(tokens, width, experts, topk)) return -1;
+    return (int64_t)(prefill_ws(tokens, width, ff, experts, topk).rcert +
+                     route_cert_stats_offset(tokens, width, experts));
 }
 
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
@@ -1127,10 +1134,21 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         return code;
     };
     if (int rc2 = stage_mark(ctx, kStagePrefillRoute)) return bail(rc2);
-    if (int rc2 = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias, experts,
-                               topk, (float *)(ws + w.logits), (int *)ids, (float *)weights, (const float *)Wsg,
-                               (float *)(ws + w.gate)))
+    if (route_cert_applies(tokens, width, experts, topk)) {
+        // The certified router: W_r's fp16 copy here while the second stream
+        // splits X, then the approximate logits from both.
+        if (int rc2 = route_cert_prepare(ctx, (const float *)Wr, tokens, width, experts, ws + w.rcert))
+            return bail(rc2);
+        if (int rc2 = wait_aux_mark(ctx)) return bail(rc2);
+        if (int rc2 = route_cert_launch(ctx, (const float *)X, xhl, tokens, width, (const float *)Wr,
+                                        (const float *)bias, experts, topk, (int *)ids, (float *)weights,
+                                        (const float *)Wsg, (float *)(ws + w.gate), ws + w.rcert))
+            return bail(rc2);
+    } else if (int rc2 = route_launch(ctx, (const float *)X, tokens, width, (const float *)Wr, (const float *)bias,
+                                      experts, topk, (float *)(ws + w.logits), (int *)ids, (float *)weights,
+                                      (const float *)Wsg, (float *)(ws + w.gate))) {
         return bail(rc2);
+    }
     if (int rc2 = stage_mark(ctx, kStagePrefillDispatch)) return bail(rc2);
     int *offsets = (int *)(ws + w.offsets);
     int *tiles_small = (int *)(ws + w.tiles_small), *tiles_big = (int *)(ws + w.tiles_big);

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <string>
+#include <vector>
 
 #include "internal.h"
 
@@ -505,6 +506,27 @@ int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk,
     *bytes = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                          : moe_prefill_workspace(tokens, width, ff, experts, topk);
     return SM_OK;
+}
+
+int sm_moe_route_stats(sm_ctx *ctx, uint64_t workspace, int tokens, int width, int ff, int experts, int topk,
+                       uint64_t *candidates, int *fallbacks) {
+    if (!ctx || !candidates || !fallbacks) return SM_E_ARG;
+    if (ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
+    *candidates = 0;
+    *fallbacks = 0;
+    if (tokens <= kDecodeMaxTokens) return 0;
+    const int64_t off = moe_prefill_route_stats_offset(tokens, width, ff, experts, topk);
+    if (off < 0) return 0;
+    if (int rc = need(ctx, workspace, (uint64_t)off + (uint64_t)tokens * 4, "workspace")) return rc;
+    std::vector<uint32_t> st((size_t)tokens);
+    HIP_TRY(ctx, hipMemcpyAsync(st.data(), (const char *)workspace + off, (size_t)tokens * 4, hipMemcpyDeviceToHost,
+                                ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    for (uint32_t v : st) {
+        *candidates += v & 0xffffu;
+        *fallbacks += (v >> 16) & 1u;
+    }
+    return tokens;
 }
 
 int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,

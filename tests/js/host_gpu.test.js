@@ -4,8 +4,10 @@
 // src/prefill.js:52-78), both against the CPU oracle's results, which
 // tests/test_js_host.py computes for the same seeded layers and inputs and
 // passes in the directory named by argv[2] (manifest.json + raw arrays).
-// Routed IDs must match bit for bit, routing weights to the bit, layer
-// outputs within |a - e| <= 1e-4 + 1e-3 |e|.
+// Routed IDs must match bit for bit, routing weights to the bit (within
+// 1e-6 relative for a fused prompt of 512 tokens or more, whose certified
+// router forms the sum of exponentials from approximate logits away from the
+// top-k boundary), layer outputs within |a - e| <= 1e-4 + 1e-3 |e|.
 import assert from 'assert';
 import fs from 'fs';
 import path from 'path';
@@ -53,7 +55,12 @@ for (const c of manifest.cases) {
             await backend.idle();
             const ids = await backend.read(r.ids), w = await backend.read(r.weights), y = await backend.read(r.y);
             assert.deepStrictEqual(Array.from(ids), Array.from(load(c.name + '_ids.bin', Int32Array)));
-            assert.deepStrictEqual(bits(w), bits(load(c.name + '_w.bin', Float32Array)));
+            const ew = load(c.name + '_w.bin', Float32Array);
+            if (fused && c.tokens >= 512) {
+                for (let i = 0; i < ew.length; i++)
+                    if (!(Math.abs(w[i] - ew[i]) <= 1e-6 * Math.abs(ew[i])))
+                        throw Error(c.name + ': weight ' + i + ' is ' + w[i] + ', expected ' + ew[i]);
+            } else assert.deepStrictEqual(bits(w), bits(ew));
             const ey = load(c.name + '_y.bin', Float32Array), rows = c.checkRows || [];
             let worst;
             if (rows.length) {

@@ -1,14 +1,15 @@
 """The fused MoE path at the real model's geometry (src/model.js:4-6: hidden
 2560, expert ff 640, 512 experts, top-10 + shared, Q2 blobs of 1,382,400
-bytes) on the GPU against the CPU oracle: routed IDs and routing weights
-bit-exact for every token, outputs of all (or a sample of) tokens within
+bytes) on the GPU against the CPU oracle: routed IDs bit-exact for every
+token, routing weights bit-exact below 512 tokens and within 1e-6 relative
+from there on (the certified batch router), outputs of every token within
 |a - e| <= 1e-4 + 1e-3 |e|. The same kernels run both geometries; these
 cases cover the decode kernels with and without a token dimension, the
 16-row tiles of small batches and the 64-row tiles of prompts."""
 import numpy as np
 import pytest
 
-from conftest import tol_ok
+from conftest import tol_ok, weights_ok
 from stratacuda_amd import workload as wl
 
 pytestmark = pytest.mark.gpu
@@ -28,9 +29,9 @@ def test_real_blob_layout(real_layer):
     assert real_layer.stride >= 1382400 and real_layer.stride % 256 == 0
 
 
-@pytest.mark.parametrize("tokens,bias,sample", [(1, False, 1), (1, True, 1), (8, False, 8), (24, False, 6),
-                                                (40, False, 6), (512, False, 12), (2048, True, 12)])
-def test_real_geometry_layer(backend, oracle, real_layer, tokens, bias, sample):
+@pytest.mark.parametrize("tokens,bias", [(1, False), (1, True), (8, False), (24, False), (40, False), (512, False),
+                                         (2048, True)])
+def test_real_geometry_layer(backend, oracle, real_layer, tokens, bias):
     layer = real_layer
     X = backend.alloc(tokens * W, "f32", zero=False)
     backend.synth_normal(X, tokens * W, layer.seed + 500 + tokens, wl.STREAM_INPUT, 1.0)
@@ -46,14 +47,9 @@ def test_real_geometry_layer(backend, oracle, real_layer, tokens, bias, sample):
         logits = (logits.reshape(tokens, E) + b).reshape(-1)
     rids, rw = oracle.router(logits, E, K, tokens)
     assert np.array_equal(got_ids, rids)
-    assert np.array_equal(got_w.view(np.uint32), rw.view(np.uint32))
-    rng = np.random.default_rng(tokens)
-    pick = np.sort(rng.choice(tokens, min(sample, tokens), replace=False))
-    sub_ids = got_ids.reshape(tokens, K)[pick].reshape(-1)
-    host = wl.host_layer(oracle, 0, width=W, ff=F, experts=E, base_seed=wl.BASE_SEED + 1, expert_ids=sub_ids)
-    xs = xh.reshape(tokens, W)[pick].reshape(-1)
-    eY, eids, _ = oracle.moe_layer(xs, len(pick), host["Wr"], host["arena"], host["stride"], host["shared"],
+    assert weights_ok(tokens, got_w, rw)
+    host = wl.host_layer(oracle, 0, width=W, ff=F, experts=E, base_seed=wl.BASE_SEED + 1, expert_ids=got_ids)
+    eY, eids, _ = oracle.moe_layer(xh, tokens, host["Wr"], host["arena"], host["stride"], host["shared"],
                                    host["Wsg"], W, F, E, K, bias=b)
-    assert np.array_equal(eids, sub_ids)
-    gy = got_y.reshape(tokens, W)[pick].reshape(-1)
-    assert tol_ok(gy, eY), "max abs err %g" % np.abs(gy - eY).max()
+    assert np.array_equal(eids, got_ids)
+    assert tol_ok(got_y, eY), "max abs err %g" % np.abs(got_y - eY).max()
