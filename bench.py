@@ -152,9 +152,12 @@ def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefi
         ms = be.event_elapsed_ms(8, 9) / prefill_reps
         distinct = len(np.unique(be.read(ids)))
         lb, lf = layer_bytes(W, F, E, K, T, distinct), layer_flops(W, F, E, K, T)
+        cert = be.route_stats(ws, T, W, F, E, K)
         out["prefill T=%d%s" % (T, " zipf" if zipf else "")] = {
             "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_layer": round(ms, 4), "distinct_experts": int(distinct),
-            "hbm_frac": round(lb / (ms * 1e-3) / PEAK_HBM, 4), "mfma_layer_frac": round(lf / (ms * 1e-3) / PEAK_MFMA_F16, 4)}
+            "hbm_frac": round(lb / (ms * 1e-3) / PEAK_HBM, 4), "mfma_layer_frac": round(lf / (ms * 1e-3) / PEAK_MFMA_F16, 4),
+            "route_candidates_per_token": round(cert[0] / T, 2) if cert else None,
+            "route_fallback_tokens": cert[1] if cert else None}
         for b in (X, Y, ids, w, ws) + ((bias,) if bias is not None else ()):
             be.free(b)
     for s_ in slots:
@@ -609,7 +612,7 @@ def flat_prefill(case, r, W, F, E, K):
             "combine_us": stage.get("prefill_combine")}
     if flat["roofline_achieved"] is not None:
         flat["roofline_achieved"] = round(flat["roofline_achieved"], 1)
-    for k in ("route_fallback_tokens", "route_candidates_per_token"):
+    for k in ("router", "route_fallback_tokens", "route_candidates_per_token"):
         if k in r:
             flat[k] = r[k]
     return flat
@@ -877,6 +880,10 @@ def main():
             ms = be.event_elapsed_ms(4, 5) / args.prefill_reps
             got = be.read(ids)
             distinct = len(np.unique(got))
+            # the certified batch router's last call on this workspace: its
+            # candidate experts per token and the tokens it sent to the exact
+            # fallback (None below the router's 512 tokens)
+            cert = be.route_stats(ws, T, W, F, E, K)
             counts = np.sort(np.bincount(got, minlength=E))[::-1]
             M = T * (K + 1)
             stages = {k: round(v[0] / max(1, v[1]) * 1e3, 2) for k, v in rep.items() if v[1]}
@@ -887,6 +894,7 @@ def main():
             prefill["T=%d%s" % (T, " zipf" if zipf else "")] = {
                 "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_layer": round(ms, 4),
                 "distinct_experts": int(distinct), "top20_share": round(float(counts[:20].sum() / got.size), 3),
+                "router": "certified (fp16 MFMA bound + exact boundary)" if cert else "exact reference order",
                 "stage_us": stages,
                 "execution": ("%d layer calls issued directly" % args.prefill_reps if args.eager else
                               "HIP graph of %d layer calls (stage_us: eager calls with events between the stages)"
@@ -900,6 +908,9 @@ def main():
                          "peak": "2.5 PFLOP/s dense fp16/bf16"},
                 "dtype": "f32 in/out; experts on fp16 MFMA (exact fp16 weights, activations split hi+lo), f32 accumulate",
             }
+            if cert:
+                prefill["T=%d%s" % (T, " zipf" if zipf else "")].update(
+                    route_candidates_per_token=round(cert[0] / T, 2), route_fallback_tokens=cert[1])
         return prefill
 
     def section_stack():
@@ -1014,7 +1025,7 @@ def main():
         for i, (case, r) in enumerate((k, v) for k, v in detail.items() if isinstance(v, dict) and "ms_per_layer" in v):
             key = "prefill" if i == 0 else "prefill_" + case.replace("=", "").replace(" ", "_")
             out[key] = flat_prefill(case, r, W, F, E, K)
-    for flag, name, fn in ((True, "prefill", section_prefill), (args.no_stack, "stack", section_stack),
+    for flag, name, fn in ((args.no_stack, "stack", section_stack),
                            (args.no_real, "real_model", lambda: real_model(be, wl, np, capture, replay, release)),
                            (args.no_dense, "dense_formats", lambda: dense_formats(be, np, capture, replay, release)),
                            (args.no_pack, "pack_load", section_pack), (args.no_prompt, "prompt", section_prompt)):

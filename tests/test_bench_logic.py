@@ -119,6 +119,9 @@ def test_flat_prefill_is_scalars_only():
     f = bench.flat_prefill("T=512", r, 2048, 512, 512, 10)
     assert all(not isinstance(v, (dict, list)) for v in f.values())
     assert f["roofline_bound"] == "hbm" and f["roofline_frac"] == 0.1993 and f["route_us"] == 60.0
-    z = bench.flat_prefill("T=2048 zipf", dict(r, ms_per_layer=0.5), 2048, 512, 512, 10)
+    assert "route_fallback_tokens" not in f
+    z = bench.flat_prefill("T=2048 zipf", dict(r, ms_per_layer=0.5, router="certified", route_fallback_tokens=0,
+                                               route_candidates_per_token=11.3), 2048, 512, 512, 10)
+    assert z["route_fallback_tokens"] == 0 and z["route_candidates_per_token"] == 11.3
     assert z["roofline_bound"] == "mfma" and z["roofline_unit"] == "TFLOP/s"
     assert abs(z["roofline_achieved"] - 36.5e9 / 0.5e-3 / 1e12) < 0.1
