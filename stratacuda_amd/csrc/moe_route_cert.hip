@@ -39,6 +39,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "internal.h"
 #include "strata_device.h"
 
@@ -134,13 +136,28 @@ __device__ __forceinline__ void approx_sync() {
 
 template <int WM, int GS>
 __global__ void __launch_bounds__(256) k_route_approx(const _Float16 *__restrict__ Xhl, const _Float16 *__restrict__ Wh,
-                                                      float *__restrict__ P, int tokens, int width, int experts) {
+                                                      float *__restrict__ P, int tokens, int width, int experts,
+                                                      int xl_tiles_e, int xl_tiles_t, int xl_splits) {
     constexpr int WN = 4 / WM, TM = 32 * WM, TN = 32 * WN, ROWS = TM + TN;
     constexpr int PER = ROWS * 8 / 256;  // DMA parts per thread per group
     static_assert(ROWS * 8 % 256 == 0 && ROWS <= kApproxStageRows, "stage shape");
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int e0 = blockIdx.x * TN, t0 = blockIdx.y * TM, ks = blockIdx.z;
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    if (xl_tiles_e) {
+        // One-dimensional grid in an XCD-aware order: block L runs on XCD
+        // L % 8, and the xl_tiles_e expert tiles of one (token tile, split)
+        // pair are consecutive blocks of one XCD, so that XCD's L2 fetches
+        // the pair's activation rows once (the grid is padded to a multiple
+        // of 8 pairs; blocks past the last pair return).
+        const int L = blockIdx.x, slot = L >> 3;
+        const int pair = (slot / xl_tiles_e) * 8 + (L & 7);
+        if (pair >= xl_tiles_t * xl_splits) return;
+        bx = slot % xl_tiles_e;
+        by = pair % xl_tiles_t;
+        bz = pair / xl_tiles_t;
+    }
+    const int e0 = bx * TN, t0 = by * TM, ks = bz;
     const int G = width / 64, g0 = ks * GS;
 
     // Part c = tid + 256 i lands in LDS slot c: row c / 8 (token rows first),
@@ -333,13 +350,15 @@ __device__ __forceinline__ void enqueue_fallback(const CertArgs &a, int t, int n
 // the GPU at once, 2 for large ones (2048 tokens then run in one round
 // instead of two).
 template <int NJ, int WPT>
-__global__ void __launch_bounds__(64 * WPT) k_route_certify(CertArgs a) {
+__global__ void __launch_bounds__(64 * WPT) __attribute__((amdgpu_waves_per_eu(WPT == 2 && NJ <= 32 ? 4 : 2)))
+k_route_certify(CertArgs a) {
     constexpr int NT = 64 * WPT;
     __shared__ uint64_t s_tab[32];
     __shared__ sm::RouterScratch s_router;
     __shared__ CertScratch s;
     __shared__ int s_ids[32];
-    __shared__ float s_x[kCertMaxWidth];
+    __shared__ __attribute__((aligned(16))) float s_x[kCertMaxWidth];
+    __shared__ float s_norm[2 * WPT];
 #ifdef SM_CERT_TRACE
     __shared__ uint64_t s_marks[16];
     if (threadIdx.x < 16) s_marks[threadIdx.x] = 0;
@@ -349,28 +368,66 @@ __global__ void __launch_bounds__(64 * WPT) k_route_certify(CertArgs a) {
     const int t = blockIdx.x, E = a.experts, K = a.topk;
     if (wave == 0) CERT_MARK(0);
     const float *x = a.X + (int64_t)t * a.width;
-    sm::fill_exp_table(s_tab);
     // Wave 0's loads of the approximate logits first (every split's partial
-    // before any sum; ks <= 4), then the token's x row into LDS once for the
-    // block (each wave reading it from memory would be four times the
-    // traffic of the whole launch's first burst).
+    // before any sum; one uniform branch on the split count, straight-line
+    // loads inside it; the bias row, or any row when there is none, loaded
+    // unconditionally), then the token's x row by every thread in 16-byte
+    // loads (clamped, so that one wait covers them all), into LDS once for
+    // the block (each wave reading it from memory would be WPT times the
+    // traffic of the launch's first burst). The x norms are formed from the
+    // same registers, every thread over its own elements. The exponential
+    // table is written while the loads are in flight.
     float qp[8][kCertMaxSplits], r2v[8], bv[8];
     if (wave == 0) {
+        const float *brow = a.bias ? a.bias : a.rn2;
+        auto load = [&](auto nsplit) {
+            constexpr int NS = decltype(nsplit)::value;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int e = min(lane + 64 * j, E - 1);
+            for (int j = 0; j < 8; j++) {
+                const int e = min(lane + 64 * j, E - 1);
 #pragma unroll
-            for (int k = 0; k < kCertMaxSplits; k++)
-                if (k < a.ks) qp[j][k] = a.P[((int64_t)k * a.tokens + t) * E + e];
-            r2v[j] = a.rn2[e];
-            bv[j] = a.bias ? a.bias[e] : 0.0f;
-        }
+                for (int k = 0; k < NS; k++) qp[j][k] = a.P[((int64_t)k * a.tokens + t) * E + e];
+#pragma unroll
+                for (int k = NS; k < kCertMaxSplits; k++) qp[j][k] = 0.0f;
+                r2v[j] = a.rn2[e];
+                bv[j] = brow[e];
+            }
+        };
+        if (a.ks == 1) load(std::integral_constant<int, 1>());
+        else if (a.ks == 2) load(std::integral_constant<int, 2>());
+        else if (a.ks == 3) load(std::integral_constant<int, 3>());
+        else load(std::integral_constant<int, kCertMaxSplits>());
     }
 #ifdef SM_CERT_TRACE
     if (wave == 0) CERT_MARK(12);
+#endif
+    constexpr int XV = (kCertMaxWidth / 4 + NT - 1) / NT;
+    const int nx4 = a.width / 4;
+    float4 xr[XV];
+#pragma unroll
+    for (int u = 0; u < XV; u++) xr[u] = ((const float4 *)x)[min(tid + NT * u, nx4 - 1)];
+    sm::fill_exp_table(s_tab);
+    {
+        float ss = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < XV; u++) {
+            if (tid + NT * u < nx4) {
+                const float4 v = xr[u];
+                ss = ss + (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+                s1 = s1 + (fabsf(v.x) + fabsf(v.y)) + (fabsf(v.z) + fabsf(v.w));
+                ((float4 *)s_x)[tid + NT * u] = v;
+            }
+        }
+        ss = sm::tree_sum64(ss);
+        s1 = sm::tree_sum64(s1);
+        if (lane == 0) {
+            s_norm[wave] = ss;
+            s_norm[WPT + wave] = s1;
+        }
+    }
+#ifdef SM_CERT_TRACE
     if (wave == 0) CERT_MARK_LOADED(13);
 #endif
-    for (int i = tid; i < a.width; i += NT) s_x[i] = x[i];
     __syncthreads();
     if (wave == 0) CERT_MARK(14);
     float xv[NJ > 0 ? NJ : 1];
@@ -388,7 +445,7 @@ __global__ void __launch_bounds__(64 * WPT) k_route_certify(CertArgs a) {
             const int e = lane + 64 * j;
             float v = -3.402823e38f;
             if (e < E) {
-                const float b = bv[j];
+                const float b = a.bias ? bv[j] : 0.0f;
                 float p = qp[j][0];
 #pragma unroll
                 for (int k = 1; k < kCertMaxSplits; k++)
@@ -403,24 +460,14 @@ __global__ void __launch_bounds__(64 * WPT) k_route_certify(CertArgs a) {
             s.a[e] = v;
         }
         CERT_MARK_LOADED(1);
-        float ss = 0.0f, s1 = 0.0f;
-        if (NJ > 0) {
+        float ss = s_norm[0], s1 = s_norm[WPT];
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                ss = ss + xv[j] * xv[j];
-                s1 = s1 + fabsf(xv[j]);
-            }
-        } else {
-            for (int i = lane; i < a.width; i += 64) {
-                const float v = s_x[i];
-                ss = ss + v * v;
-                s1 = s1 + fabsf(v);
-            }
+        for (int w = 1; w < WPT; w++) {
+            ss = ss + s_norm[w];
+            s1 = s1 + s_norm[WPT + w];
         }
         // sums in any order: the factors 1.002 below cover their rounding
         // (widths <= 2^13)
-        ss = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sm::tree_sum64(ss))));
-        s1 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sm::tree_sum64(s1))));
         rn = sm::wave_max(rn);
         amax = sm::wave_max(amax);
         bmax = sm::wave_max(bmax);
@@ -484,21 +531,20 @@ __global__ void __launch_bounds__(64 * WPT) k_route_certify(CertArgs a) {
     // ---- exact logits of the candidates (in place of their approximate
     // ones) and of the shared-expert gate row, all waves
     const int nc = s.nc;
-    exact_rows<NJ>(
-        xv, s_x, a.width, nc + (a.Wsg ? 1 : 0), wave, WPT,
-        [&](int i, int &e) -> const float * {
-            if (i >= nc) {
-                e = -1;
-                return a.Wsg;
-            }
-            e = s.cand[i];
-            return a.Wr + (int64_t)e * a.width;
-        },
-        [&](int e, float v) {
-            if (lane != 0) return;
-            if (e < 0) a.gate_out[t] = v;
-            else s.a[e] = a.bias ? v + a.bias[e] : v;
-        });
+    auto cand_row = [&](int i, int &e) -> const float * {
+        if (i >= nc) {
+            e = -1;
+            return a.Wsg;
+        }
+        e = s.cand[i];
+        return a.Wr + (int64_t)e * a.width;
+    };
+    auto cand_put = [&](int e, float v) {
+        if (lane != 0) return;
+        if (e < 0) a.gate_out[t] = v;
+        else s.a[e] = a.bias ? v + a.bias[e] : v;
+    };
+    exact_rows<NJ>(xv, s_x, a.width, nc + (a.Wsg ? 1 : 0), wave, WPT, cand_row, cand_put);
     CERT_MARK(4 + wave);
     __syncthreads();
     if (wave == 0) CERT_MARK(8);
@@ -723,13 +769,21 @@ int route_cert_launch(sm_ctx *ctx, const float *X, const _Float16 *Xhl, int toke
     const CertWs w = cert_ws(tokens, width, experts);
     float *P = (float *)(ws + w.P), *rn2 = (float *)(ws + w.rn2);
     const _Float16 *Wh = (const _Float16 *)(ws + w.Wh);
-    const dim3 g1((unsigned)p.tiles_e, (unsigned)p.tiles_t, (unsigned)p.ks);
-    using KA = void (*)(const _Float16 *, const _Float16 *, float *, int, int, int);
+    // From 1,024 tokens on the activation rows outweigh W_r's copy: the
+    // XCD-aware order keeps each token tile on one XCD (8 x W_r's 2 MiB
+    // copy fetched into the eight L2s, instead of every token tile into up
+    // to eight).
+    const bool xlocal = p.wm == 2;
+    const int pairs = p.tiles_t * p.ks, padded = (pairs + 7) / 8 * 8;
+    const dim3 g1 = xlocal ? dim3((unsigned)(padded * p.tiles_e))
+                           : dim3((unsigned)p.tiles_e, (unsigned)p.tiles_t, (unsigned)p.ks);
+    using KA = void (*)(const _Float16 *, const _Float16 *, float *, int, int, int, int, int, int);
     const int gi = p.gspan == 8 ? 0 : p.gspan == 16 ? 1 : p.gspan == 10 ? 2 : 3;
     static const KA by_span[2][4] = {
         {k_route_approx<1, 8>, k_route_approx<1, 16>, k_route_approx<1, 10>, k_route_approx<1, 20>},
         {k_route_approx<2, 8>, k_route_approx<2, 16>, k_route_approx<2, 10>, k_route_approx<2, 20>}};
-    by_span[p.wm - 1][gi]<<<g1, 256, 0, ctx->stream>>>(Xhl, Wh, P, tokens, width, experts);
+    by_span[p.wm - 1][gi]<<<g1, 256, 0, ctx->stream>>>(Xhl, Wh, P, tokens, width, experts, xlocal ? p.tiles_e : 0,
+                                                       p.tiles_t, p.ks);
     if (int rc = launched(ctx)) return rc;
     CertArgs a;
     a.X = X;
