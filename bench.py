@@ -106,6 +106,8 @@ def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefi
     out = {"workload": "single MoE layer, hidden 2560, ff 640, 512 experts, top-10 + shared, Q2 (1,382,400-byte "
                        "blobs), %d resident layers rotated" % layers,
            "decode_T1": {"tokens_per_s": round(1e6 / us, 1), "us_per_step": round(us, 3),
+                         "execution": "one k_decode_fused launch per layer (kernels: the three-kernel path's stages, "
+                                      "each alone)",
                          "hbm": {"bytes_per_step": step_bytes, "frac": round(step_bytes / (us * 1e-6) / PEAK_HBM, 4)}}}
     kb = decode_kernel_bytes(W, F, E, K)
     kern = {}

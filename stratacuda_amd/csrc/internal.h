@@ -56,7 +56,8 @@ struct sm_ctx {
     // switch (sm_fused_test_hooks); a pinned host word its kernels set when a
     // wait gives up (read after every synchronisation, cleared by
     // sm_fused_reset).
-    bool fused_capable = false;
+    bool fused_capable = false;     // hidden 2048 / ff 512
+    bool fused_capable_rg = false;  // hidden 2560 / ff 640
     uint32_t fused_spin_limit = 0, fused_withhold = 0;
     uint32_t *fault_host = nullptr, *fault_dev = nullptr;  // host pointer, and its device address
     // Captured graphs kept beside their executables until sm_graph_free.
@@ -107,8 +108,8 @@ constexpr int kFusedSyncBase = 1024;
 uint32_t fused_fault_word();
 uint32_t fused_sync_words();
 // Whether kFusedBlocks blocks fit at once on `compute_units` CUs holding
-// `blocks_per_cu` blocks each; fused_decode_init sets ctx->fused_capable
-// from the device's CU count and the kernel's occupancy.
+// `blocks_per_cu` blocks each; fused_decode_init sets ctx->fused_capable and
+// ctx->fused_capable_rg from the device's CU count and the kernels' occupancy.
 bool fused_fits(int compute_units, int blocks_per_cu);
 int fused_decode_init(sm_ctx *ctx);
 inline bool stage_on(const sm_ctx *ctx, int stage) { return (ctx->stage_mask >> stage) & 1u; }

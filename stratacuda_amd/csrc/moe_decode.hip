@@ -737,7 +737,7 @@ __global__ void __launch_bounds__(256) k_decode_down_wide(const float *__restric
 // device's CU count times its occupancy (one block per CU) covers them.
 constexpr int kFusedBlocks = 256, kFusedWaves = 8;
 constexpr int kFusedRows = 3;  // hidden rows per wave: ceil(11 x 512 / 2048)
-constexpr int kFusedWidth = 2048, kFusedFF = 512, kFusedMaxTopk = 10;
+constexpr int kFusedMaxTopk = 10;
 constexpr int kFusedCollector = kFusedBlocks - 1;  // block whose wave 7 collects the flags
 constexpr uint32_t kFusedSpinLimit = 1u << 20;
 // Word offsets in the synchronisation area (ctx->counters + kFusedSyncBase):
@@ -917,16 +917,35 @@ __device__ uint64_t g_fused_trace[kFusedBlocks * 32];
     do { } while (0)
 #endif
 
-template <bool NORM>
+// W x F: hidden 2048 / ff 512 (the benchmark geometry) or hidden 2560 / ff
+// 640 (the real model's, RG below). RG differs in three places: 40 groups
+// per gate/up row (groups 32-39 spread one (row, group) pair per lane, as
+// in k_decode_gate_up<true>), 7,040 hidden rows (waves 0-3 of a block take
+// four, waves 4-7 three: at most seven per SIMD), and 10 output rows per
+// block whose 1,100 (slot, row, group) down products are spread over the
+// block's threads with every slot's hidden vector in LDS, summed per row in
+// group order as k_decode_down10 does, so both geometries give the bits of
+// their three-kernel paths.
+template <bool NORM, int W, int F>
 __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs a) {
-    constexpr int G = kFusedWidth / 64, GD = kFusedFF / 64, ROW_BYTES = kFusedWidth / 4;
+    static_assert((W == 2048 && F == 512) || (W == 2560 && F == 640), "fused geometries");
+    constexpr bool RG = W == 2560;
+    constexpr int G = W / 64, GD = F / 64, ROW_BYTES = W / 4;
+    constexpr int DR = W / kFusedBlocks;  // output rows per block: 8, or 10 for RG
+    constexpr int RB = RG ? 4 : kFusedRows;  // hidden rows per wave at most
+    constexpr int RG_ITEMS = 4 * 4 + 3 * 4;  // RG hidden rows per block
+    constexpr int RG_PAIRS = (kFusedMaxTopk + 1) * DR * GD;  // RG down products per block
     __shared__ __attribute__((aligned(16))) uint32_t s_rec[G * kRecPitch];
     __shared__ uint64_t s_tab[32];
     __shared__ sm::RouterScratch s_router;
     __shared__ int s_ids[32];
     __shared__ float s_w[32];
-    __shared__ float s_parts[(kFusedMaxTopk + 2) * 8];
-    __shared__ __attribute__((aligned(16))) float s_h[kFusedWaves][2][8 * DN_PITCH];
+    __shared__ float s_parts[(kFusedMaxTopk + 2) * DR];
+    __shared__ __attribute__((aligned(16))) float s_h[RG ? 1 : kFusedWaves][2][8 * DN_PITCH];
+    // RG: every slot's hidden vector (group g of slot k at (k GD + g) DN_PITCH)
+    // and the down products v[slot][row][group]
+    __shared__ __attribute__((aligned(16))) float s_hid[RG ? (kFusedMaxTopk + 1) * GD * DN_PITCH : 1];
+    __shared__ float s_red[RG ? RG_PAIRS : 1];
     __shared__ uint32_t s_arrive;
     __shared__ float s_sig;
     __shared__ int s_ok, s_spec, s_reload, s_staged, s_selected, s_recs;
@@ -963,13 +982,13 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
 #pragma unroll
     for (int j = 0; j < G; j++) xv[j] = a.X[lane + 64 * j];
     float xres = 0.0f;  // the block entry's residual for combine thread tid < 8
-    if (NORM) xres = a.X[min(b * 8 + (tid & 7), kFusedWidth - 1)];
+    if (NORM) xres = a.X[RG ? min(b * DR + min(tid, DR - 1), W - 1) : min(b * 8 + (tid & 7), W - 1)];
     const bool router = wave < 2;
     const int row = b + kFusedBlocks * wave;
     const bool gate_wave = b == 0 && wave == 2;
     // One weight-row load site for the router row and the shared gate vector
     // (the registers then have a single writer on every path).
-    const float *wsrc = router ? a.Wr + (int64_t)min(row, experts - 1) * kFusedWidth : gate_wave ? a.Wsg : nullptr;
+    const float *wsrc = router ? a.Wr + (int64_t)min(row, experts - 1) * W : gate_wave ? a.Wsg : nullptr;
     float wv[G];
     if (wsrc) {
 #pragma unroll
@@ -984,7 +1003,7 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
 #pragma unroll
         for (int j = 0; j < G; j++) ss = ss + xv[j] * xv[j];
         ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm::tree_sum64(ss)), 0));
-        const float inv = 1.0f / sqrtf(ss / (float)kFusedWidth + a.eps);
+        const float inv = 1.0f / sqrtf(ss / (float)W + a.eps);
 #pragma unroll
         for (int j = 0; j < G; j++) xv[j] = (xv[j] * inv) * gv[j];
     }
@@ -1127,18 +1146,30 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     if (wave == 0) FUSED_MARK(12);
     ok = s_ok;
 
-    // ---- phase B: kFusedRows hidden rows of the 11 x 512 (item = slot x 512
-    // + row; the shared expert is slot topk). Code loads from s_ids.
+    // ---- phase B: the wave's hidden rows items base .. base + nrow - 1 of
+    // the 11 x F (item = slot x F + row; the shared expert is slot topk):
+    // three per wave, or for RG four (waves 0-3) or three (waves 4-7), 28
+    // per block. Code loads from s_ids; a row past nrow reloads the last one.
     const int rr = lane >> 3, g8 = lane & 7;
     const int drow = b * 8 + rr;
-    uint4 c[kFusedRows];
-    uint32_t sb[kFusedRows];
-    bool rok[kFusedRows];
+    const int nitems = nslot * F;
+    const int nrow = RG ? (wave < 4 ? 4 : 3) : kFusedRows;
+    const int base = RG ? b * RG_ITEMS + (wave < 4 ? 4 * wave : 16 + 3 * (wave - 4)) : gw * kFusedRows;
+    // RG: the lane's (row, group) pair of groups 32-39: group g2 of the
+    // wave's row r2 whose item is gl / 8 modulo 4. k_decode_gate_up<true>
+    // gives item i's pairs to lanes 8 (i % 4) .. + 7 (its waves start at
+    // multiples of 4), and the lane a product lands on fixes the rounding of
+    // the half-wave sum; a wave's rows are at most 4 consecutive items, so
+    // each residue is at most one row (r2 >= nrow: no row, the lane idles).
+    const int r2 = ((gl >> 3) - base) & 3, g2 = 32 + (gl & 7);
+    uint4 c[RB], ce;
+    uint32_t sb[RB], sbe;
+    bool rok[RB];
     auto issue_codes = [&]() {
 #pragma unroll
-        for (int r = 0; r < kFusedRows; r++) {
-            const int item = min(gw * kFusedRows + r, nslot * kFusedFF - 1);
-            const int k = item / kFusedFF, j = item - k * kFusedFF;
+        for (int r = 0; r < RB; r++) {
+            const int item = min(base + (RG ? min(r, nrow - 1) : r), nitems - 1);
+            const int k = item / F, j = item - k * F;
             const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, k < topk ? s_ids[k] : 0, k, topk, experts);
             rok[r] = blob != nullptr;
             blob = blob ? blob : a.shared;
@@ -1146,13 +1177,24 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
             c[r] = load_codes(blob + wrow * ROW_BYTES + gl * 16);
             sb[r] = *(const uint16_t *)(blob + a.gu_scales + (wrow * G + gl) * 2);
         }
+        if constexpr (RG) {
+            const int item = min(base + min(r2, nrow - 1), nitems - 1);
+            const int k = item / F, j = item - k * F;
+            const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, k < topk ? s_ids[k] : 0, k, topk, experts);
+            blob = blob ? blob : a.shared;  // (its row's rok covers it)
+            const uint64_t wrow = 2 * (uint64_t)j + half;
+            ce = load_codes(blob + wrow * ROW_BYTES + g2 * 16);
+            sbe = *(const uint16_t *)(blob + a.gu_scales + (wrow * G + g2) * 2);
+        }
     };
     issue_codes();
-    // The activation records of the lane's group into registers while the
-    // codes are in flight (once the six record waves have written them).
+    // The activation records of the lane's group (RG: and of its pair's
+    // group) into registers while the codes are in flight (once the six
+    // record waves have written them).
     lds_wait_count(&s_recs, kFusedWaves - 2);
-    XQ xq;
+    XQ xq, xq2;
     load_xq_lds(s_rec, gl, xq);
+    if constexpr (RG) load_xq_lds(s_rec, g2, xq2);
     // Wave 1 confirms the candidate from the probabilities (or replaces it:
     // the loads are then issued again) and forms the weights; the barrier
     // orders LDS only, so every wave's code loads stay in flight.
@@ -1166,13 +1208,23 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     if (s_reload) issue_codes();
     {
         FUSED_MARK_LOADED(16 + wave);
-        float acc[kFusedRows];
+        float acc[RB];
+        if constexpr (RG) {
+            // k_decode_gate_up<true>'s sums: group gl by fma onto 0, then the
+            // pair's product added to its row (and +0 to the others)
 #pragma unroll
-        for (int r = 0; r < kFusedRows; r++) acc[r] = sm::half_bits(sb[r]) * dot64_q(c[r], xq);
+            for (int r = 0; r < RB; r++) acc[r] = fmaf(sm::half_bits(sb[r]), dot64_q(c[r], xq), 0.0f);
+            const float v = sm::half_bits(sbe) * dot64_q(ce, xq2);
+#pragma unroll
+            for (int r = 0; r < RB; r++) acc[r] += r == r2 ? v : 0.0f;
+        } else {
+#pragma unroll
+            for (int r = 0; r < RB; r++) acc[r] = sm::half_bits(sb[r]) * dot64_q(c[r], xq);
+        }
         // row r's gate and up sums (lanes 31 and 63) go to lane r: one SiLU
         float g = 0.0f, u = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kFusedRows; r++) {
+        for (int r = 0; r < RB; r++) {
             const float v = sm::half32_sum(acc[r]);
             const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
             const float ur = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
@@ -1181,10 +1233,10 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         }
         bool mine_ok = true;
 #pragma unroll
-        for (int r = 0; r < kFusedRows; r++) mine_ok = lane == r ? rok[r] : mine_ok;
+        for (int r = 0; r < RB; r++) mine_ok = lane == r ? rok[r] : mine_ok;
         const float h = mine_ok ? sm::silu(g, s_tab) * u : __builtin_nanf("");
-        const int item = gw * kFusedRows + lane;
-        if (lane < kFusedRows && item < nslot * kFusedFF) store_coherent(a.hidden + item, h);
+        const int item = base + lane;
+        if (lane < nrow && item < nitems) store_coherent(a.hidden + item, h);
     }
     stores_complete();
     FUSED_MARK(24 + wave);
@@ -1193,17 +1245,31 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         __hip_atomic_store(a.sync + kFusedFlagsB + b, launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // The down codes of this block's 8 output rows for the wave's slots
     // (wave and wave + 8): in flight while the hidden rows come in.
-    uint4 dc[2];
-    uint32_t dsb[2];
-    bool dok[2];
+    // RG: the down codes of the thread's (slot, row, group) products
+    // p = tid, tid + 512, tid + 1024 (p < RG_PAIRS; slot p / 100, row
+    // (p / 10) % 10, group p % 10), clamped to the last product.
+    constexpr int DQ = RG ? (RG_PAIRS + 64 * kFusedWaves - 1) / (64 * kFusedWaves) : 2;
+    uint4 dc[DQ];
+    uint32_t dsb[DQ];
+    bool dok[DQ];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int s = min(wave + kFusedWaves * q, nslot - 1);
+    for (int q = 0; q < DQ; q++) {
+        int s, row, grp;
+        if constexpr (RG) {
+            const int p = min(tid + 64 * kFusedWaves * q, RG_PAIRS - 1);
+            s = min(p / (DR * GD), nslot - 1);
+            row = b * DR + (p / GD) % DR;
+            grp = p % GD;
+        } else {
+            s = min(wave + kFusedWaves * q, nslot - 1);
+            row = drow;
+            grp = g8;
+        }
         const uint8_t *blob = slot_blob(a.arena, a.stride, a.shared, s < topk ? s_ids[s] : 0, s, topk, experts);
         dok[q] = blob != nullptr;
         blob = blob ? blob : a.shared;
-        dc[q] = load_codes(blob + a.down_codes + (uint64_t)drow * (kFusedFF / 4) + g8 * 16);
-        dsb[q] = *(const uint16_t *)(blob + a.down_scales + ((uint64_t)drow * GD + g8) * 2);
+        dc[q] = load_codes(blob + a.down_codes + (uint64_t)row * (F / 4) + grp * 16);
+        dsb[q] = *(const uint16_t *)(blob + a.down_scales + ((uint64_t)row * GD + grp) * 2);
     }
     // The collector runs whatever its own block's state: every block writes
     // its flag (a block that gave up included), and only the collector
@@ -1234,100 +1300,161 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     }
     __syncthreads();
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-        a.hidden, (short)0, (int)((uint32_t)nslot * kFusedFF * 4), 0x00020000);
-    // lane (rr, g8) brings values 8 rr .. 8 rr + 7 of hidden group g8 of each
-    // of the wave's slots; all loads issued before any is used (a slot past
-    // the last reads the last one again)
-    float4 hq[2][2];
+        a.hidden, (short)0, (int)((uint32_t)nslot * F * 4), 0x00020000);
+    if constexpr (RG) {
+        // Every slot's hidden vector into LDS (16-byte coherent loads, all
+        // issued before any is stored), group g of slot k at (k GD + g) x
+        // DN_PITCH; then the thread's down products, each over its group
+        // from LDS (lanes of one group read the same addresses); then per
+        // (slot, row) the groups' products in group order; then the combine.
+        constexpr int N4MAX = (kFusedMaxTopk + 1) * F / 4, HQ = (N4MAX + 64 * kFusedWaves - 1) / (64 * kFusedWaves);
+        const int n4 = nitems / 4;
+        float4 hv[HQ];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int s = min(wave + kFusedWaves * q, nslot - 1);
-        const uint32_t off = (uint32_t)(s * kFusedFF + g8 * 64 + 8 * rr) * 4;
-        hq[q][0] = load16_coherent(hr, off);
-        hq[q][1] = load16_coherent(hr, off + 16);
-    }
-    // the shared expert's gate, sigmoid(gate logit), by a wave with one slot
-    if (wave == kFusedWaves - 1) {
-        const float sig = sm::sigmoid(load_coherent(a.gate), s_tab);
-        if (lane == 0) s_sig = sig;
-    }
-    // Read with the hidden rows rather than after the products: a wait that
-    // gave up in any block set the fault word before that block's flag, so
-    // before the go word; this block's own give-ups are in wave 0's `ok`
-    // (wave 0 forms the outputs).
-    const bool faulted = load_coherent_u32(fault) != 0u || !ok;
-    if (wave == 0) FUSED_MARK_LOADED(11);
-    // The wave's slots are wave and wave + 8 (two for waves 0-2 at top-10);
-    // with two, both dots run side by side (independent chains), each slot
-    // with its own exchange area. Per slot: the group sum of the hidden
-    // values (own eighth, then lanes ^ 8, ^ 16, ^ 32), the exchange (lane
-    // (rr, g8) stores values 8 rr .. 8 rr + 7 of group g8, then reads the
-    // whole group), the dot in dot64_4's order.
-    const bool two = wave + kFusedWaves < nslot;
-    float s8[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-        if (q == 1 && !two) break;
-        const float4 h0 = hq[q][0], h1 = hq[q][1];
-        float t = ((h0.x + h0.y) + (h0.z + h0.w)) + ((h1.x + h1.y) + (h1.z + h1.w));
-        t = t + sm::dpp_f32<0x128>(0.0f, t);
-        const int u = __builtin_bit_cast(int, t);
-        const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        t = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
-        const int w = __builtin_bit_cast(int, t);
-        const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-        s8[q] = __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
-        float *xh = s_h[wave][q];
-        *(float4 *)&xh[g8 * DN_PITCH + 8 * rr] = h0;
-        *(float4 *)&xh[g8 * DN_PITCH + 8 * rr + 4] = h1;
-    }
-    __builtin_amdgcn_wave_barrier();
-    // 16 hidden values of group g8 (chunk w4) from exchange area q
-    auto chunk = [&](int q, int w4, float (&x)[16]) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 v = *(const float4 *)&s_h[wave][q][g8 * DN_PITCH + 16 * w4 + 4 * i];
-            x[4 * i] = v.x;
-            x[4 * i + 1] = v.y;
-            x[4 * i + 2] = v.z;
-            x[4 * i + 3] = v.w;
+        for (int i = 0; i < HQ; i++) hv[i] = load16_coherent(hr, (uint32_t)min(tid + 64 * kFusedWaves * i, n4 - 1) * 16);
+        if (wave == kFusedWaves - 1) {
+            const float sig = sm::sigmoid(load_coherent(a.gate), s_tab);
+            if (lane == 0) s_sig = sig;
         }
-    };
-    auto word = [](const uint4 &c, int w4) { return w4 == 0 ? c.x : w4 == 1 ? c.y : w4 == 2 ? c.z : c.w; };
-    float d[2][4];
-    if (two) {
+        const bool faulted = load_coherent_u32(fault) != 0u || !ok;
+        if (wave == 0) FUSED_MARK_LOADED(11);
 #pragma unroll
-        for (int w4 = 0; w4 < 4; w4++) {
-            float x0[16], x1[16];
-            chunk(0, w4, x0);
-            chunk(1, w4, x1);
-            d[0][w4] = dot16(word(dc[0], w4), x0, 0.0f);
-            d[1][w4] = dot16(word(dc[1], w4), x1, 0.0f);
+        for (int i = 0; i < HQ; i++) {
+            const int idx = tid + 64 * kFusedWaves * i;
+            if (idx < n4) {
+                const int e = 4 * idx, k = e / F, o = e - k * F;
+                *(float4 *)&s_hid[(k * GD + (o >> 6)) * DN_PITCH + (o & 63)] = hv[i];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < DQ; q++) {
+            const int p = tid + 64 * kFusedWaves * q;
+            const int k = p / (DR * GD), grp = p % GD;
+            if (p < RG_PAIRS && k < nslot) {
+                float h[64];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float4 v = *(const float4 *)&s_hid[(k * GD + grp) * DN_PITCH + 4 * i];
+                    h[4 * i] = v.x;
+                    h[4 * i + 1] = v.y;
+                    h[4 * i + 2] = v.z;
+                    h[4 * i + 3] = v.w;
+                }
+                s_red[p] = dok[q] ? sm::half_bits(dsb[q]) * (dot64_4(dc[q], h) - sum64(h)) : __builtin_nanf("");
+            }
+        }
+        __syncthreads();
+        if (tid < nslot * DR) {
+            const float *v = &s_red[tid * GD];  // slot tid / DR, row tid % DR
+            float t = v[0];
+#pragma unroll
+            for (int j = 1; j < GD; j++) t = t + v[j];
+            s_parts[tid] = t;
+        }
+        __syncthreads();
+        if (tid < DR) {
+            const int r = b * DR + tid;
+            float value = s_parts[topk * DR + tid] * s_sig;
+            for (int k = 0; k < topk; k++) value = value + s_parts[k * DR + tid] * s_w[k];
+            if (faulted) value = __builtin_nanf("");
+            a.Y[r] = NORM ? xres + value : value;
         }
     } else {
-#pragma unroll
-        for (int w4 = 0; w4 < 4; w4++) {
-            float x0[16];
-            chunk(0, w4, x0);
-            d[0][w4] = dot16(word(dc[0], w4), x0, 0.0f);
-            d[1][w4] = 0.0f;
+        // lane (rr, g8) brings values 8 rr .. 8 rr + 7 of hidden group g8 of each
+        // of the wave's slots; all loads issued before any is used (a slot past
+        // the last reads the last one again)
+        float4 hq[2][2];
+    #pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int s = min(wave + kFusedWaves * q, nslot - 1);
+            const uint32_t off = (uint32_t)(s * F + g8 * 64 + 8 * rr) * 4;
+            hq[q][0] = load16_coherent(hr, off);
+            hq[q][1] = load16_coherent(hr, off + 16);
         }
-    }
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-        if (q == 1 && !two) break;
-        const float dot = (d[q][0] + d[q][1]) + (d[q][2] + d[q][3]);
-        float v = dok[q] ? sm::half_bits(dsb[q]) * (dot - s8[q]) : __builtin_nanf("");
-        v = sm::group8_sum(v);
-        if (g8 == 0) s_parts[(wave + kFusedWaves * q) * 8 + rr] = v;
-    }
-    __syncthreads();
-    if (tid < 8) {
-        const int r = b * 8 + tid;
-        float value = s_parts[topk * 8 + tid] * s_sig;
-        for (int k = 0; k < topk; k++) value = value + s_parts[k * 8 + tid] * s_w[k];
-        if (faulted) value = __builtin_nanf("");
-        a.Y[r] = NORM ? xres + value : value;
+        // the shared expert's gate, sigmoid(gate logit), by a wave with one slot
+        if (wave == kFusedWaves - 1) {
+            const float sig = sm::sigmoid(load_coherent(a.gate), s_tab);
+            if (lane == 0) s_sig = sig;
+        }
+        // Read with the hidden rows rather than after the products: a wait that
+        // gave up in any block set the fault word before that block's flag, so
+        // before the go word; this block's own give-ups are in wave 0's `ok`
+        // (wave 0 forms the outputs).
+        const bool faulted = load_coherent_u32(fault) != 0u || !ok;
+        if (wave == 0) FUSED_MARK_LOADED(11);
+        // The wave's slots are wave and wave + 8 (two for waves 0-2 at top-10);
+        // with two, both dots run side by side (independent chains), each slot
+        // with its own exchange area. Per slot: the group sum of the hidden
+        // values (own eighth, then lanes ^ 8, ^ 16, ^ 32), the exchange (lane
+        // (rr, g8) stores values 8 rr .. 8 rr + 7 of group g8, then reads the
+        // whole group), the dot in dot64_4's order.
+        const bool two = wave + kFusedWaves < nslot;
+        float s8[2] = {0.0f, 0.0f};
+    #pragma unroll
+        for (int q = 0; q < 2; q++) {
+            if (q == 1 && !two) break;
+            const float4 h0 = hq[q][0], h1 = hq[q][1];
+            float t = ((h0.x + h0.y) + (h0.z + h0.w)) + ((h1.x + h1.y) + (h1.z + h1.w));
+            t = t + sm::dpp_f32<0x128>(0.0f, t);
+            const int u = __builtin_bit_cast(int, t);
+            const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            t = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
+            const int w = __builtin_bit_cast(int, t);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+            s8[q] = __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
+            float *xh = s_h[wave][q];
+            *(float4 *)&xh[g8 * DN_PITCH + 8 * rr] = h0;
+            *(float4 *)&xh[g8 * DN_PITCH + 8 * rr + 4] = h1;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // 16 hidden values of group g8 (chunk w4) from exchange area q
+        auto chunk = [&](int q, int w4, float (&x)[16]) {
+    #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = *(const float4 *)&s_h[wave][q][g8 * DN_PITCH + 16 * w4 + 4 * i];
+                x[4 * i] = v.x;
+                x[4 * i + 1] = v.y;
+                x[4 * i + 2] = v.z;
+                x[4 * i + 3] = v.w;
+            }
+        };
+        auto word = [](const uint4 &c, int w4) { return w4 == 0 ? c.x : w4 == 1 ? c.y : w4 == 2 ? c.z : c.w; };
+        float d[2][4];
+        if (two) {
+    #pragma unroll
+            for (int w4 = 0; w4 < 4; w4++) {
+                float x0[16], x1[16];
+                chunk(0, w4, x0);
+                chunk(1, w4, x1);
+                d[0][w4] = dot16(word(dc[0], w4), x0, 0.0f);
+                d[1][w4] = dot16(word(dc[1], w4), x1, 0.0f);
+            }
+        } else {
+    #pragma unroll
+            for (int w4 = 0; w4 < 4; w4++) {
+                float x0[16];
+                chunk(0, w4, x0);
+                d[0][w4] = dot16(word(dc[0], w4), x0, 0.0f);
+                d[1][w4] = 0.0f;
+            }
+        }
+    #pragma unroll
+        for (int q = 0; q < 2; q++) {
+            if (q == 1 && !two) break;
+            const float dot = (d[q][0] + d[q][1]) + (d[q][2] + d[q][3]);
+            float v = dok[q] ? sm::half_bits(dsb[q]) * (dot - s8[q]) : __builtin_nanf("");
+            v = sm::group8_sum(v);
+            if (g8 == 0) s_parts[(wave + kFusedWaves * q) * 8 + rr] = v;
+        }
+        __syncthreads();
+        if (tid < 8) {
+            const int r = b * 8 + tid;
+            float value = s_parts[topk * 8 + tid] * s_sig;
+            for (int k = 0; k < topk; k++) value = value + s_parts[k * 8 + tid] * s_w[k];
+            if (faulted) value = __builtin_nanf("");
+            a.Y[r] = NORM ? xres + value : value;
+        }
     }
     if (wave == 0) FUSED_MARK(9);
 #ifdef SM_FUSED_TRACE
@@ -1389,18 +1516,23 @@ bool fused_fits(int compute_units, int blocks_per_cu) {
 }
 
 int fused_decode_init(sm_ctx *ctx) {
-    // Both instantiations have the same resources; the one-block-per-CU
-    // bound makes this 0 or 1 on a CDNA CU.
-    int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_fused<true>, 64 * kFusedWaves, 0);
-    if (e != hipSuccess) return hip_fail(ctx, e, "hipOccupancyMaxActiveBlocksPerMultiprocessor(k_decode_fused)");
-    int per_cu2 = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, k_decode_fused<false>, 64 * kFusedWaves, 0);
-    if (e != hipSuccess) return hip_fail(ctx, e, "hipOccupancyMaxActiveBlocksPerMultiprocessor(k_decode_fused)");
+    // Blocks per CU of each instantiation (the one-block-per-CU bound makes
+    // this 0 or 1 on a CDNA CU); each geometry is enabled only when both of
+    // its instantiations fit.
+    using KF = void (*)(FusedArgs);
+    const KF kernels[4] = {k_decode_fused<true, 2048, 512>, k_decode_fused<false, 2048, 512>,
+                           k_decode_fused<true, 2560, 640>, k_decode_fused<false, 2560, 640>};
+    int per_cu[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 4; i++) {
+        const hipError_t e =
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu[i], kernels[i], 64 * kFusedWaves, 0);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipOccupancyMaxActiveBlocksPerMultiprocessor(k_decode_fused)");
+    }
     int cus = 0;
-    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
+    const hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipDeviceGetAttribute(multiProcessorCount)");
-    ctx->fused_capable = fused_fits(cus, per_cu < per_cu2 ? per_cu : per_cu2);
+    ctx->fused_capable = fused_fits(cus, per_cu[0] < per_cu[1] ? per_cu[0] : per_cu[1]);
+    ctx->fused_capable_rg = fused_fits(cus, per_cu[2] < per_cu[3] ? per_cu[2] : per_cu[3]);
     ctx->fused_spin_limit = kFusedSpinLimit;
     ctx->fused_withhold = 0;
     return SM_OK;
@@ -1438,11 +1570,13 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
     float *hidden = (float *)(ws + w.hidden);
     const int blocks_per_expert = ceil_div(ff, GU_ROWS * GU_WAVES);
     uint32_t *xq = (uint32_t *)(ws + w.xq);
-    // One token at hidden 2048 / ff 512: the whole layer in one launch.
+    // One token at hidden 2048 / ff 512 or 2560 / 640: the whole layer in
+    // one launch.
     const uint32_t decode_stages = (1u << kStageDecodeRoute) | (1u << kStageDecodeGateUp) | (1u << kStageDecodeDown);
-    if (ctx->fused_capable && tokens == 1 && width == kFusedWidth && ff == kFusedFF && experts <= 2 * kFusedBlocks &&
-        topk <= kFusedMaxTopk && stage_on(ctx, kStageDecodeFused) &&
-        (ctx->stage_mask & decode_stages) == decode_stages) {
+    const bool geo_2048 = width == 2048 && ff == 512 && ctx->fused_capable;
+    const bool geo_2560 = width == 2560 && ff == 640 && ctx->fused_capable_rg;
+    if (tokens == 1 && (geo_2048 || geo_2560) && experts <= 2 * kFusedBlocks && topk <= kFusedMaxTopk &&
+        stage_on(ctx, kStageDecodeFused) && (ctx->stage_mask & decode_stages) == decode_stages) {
         if (int rc = stage_mark(ctx, kStageDecodeFused)) return rc;
         FusedArgs fa;
         fa.X = (const float *)X;
@@ -1469,7 +1603,8 @@ int moe_decode(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, 
         fa.spin_limit = ctx->fused_spin_limit;
         fa.withhold = ctx->fused_withhold;
         fa.fault_host = ctx->fault_dev;
-        const auto kf = gamma ? k_decode_fused<true> : k_decode_fused<false>;
+        const auto kf = geo_2048 ? (gamma ? k_decode_fused<true, 2048, 512> : k_decode_fused<false, 2048, 512>)
+                                 : (gamma ? k_decode_fused<true, 2560, 640> : k_decode_fused<false, 2560, 640>);
         kf<<<kFusedBlocks, 64 * kFusedWaves, 0, ctx->stream>>>(fa);
         if (int rc = launched(ctx)) return rc;
         return stage_mark(ctx, -1);

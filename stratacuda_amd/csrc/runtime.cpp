@@ -200,11 +200,12 @@ int sm_info(sm_ctx *ctx, char *buf, size_t cap) {
     int n = snprintf(buf, cap,
                      "{\"backend\":\"hip\",\"device\":%d,\"name\":\"%s\",\"arch\":\"%s\",\"computeUnits\":%d,"
                      "\"globalMemoryBytes\":%llu,\"dispatches\":%llu,\"allocatedBytes\":%llu,\"buffers\":%zu,"
-                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu,\"fusedDecode\":%s,\"fusedDecodeFault\":%lld}",
+                     "\"uploadedBytes\":%llu,\"readbackBytes\":%llu,\"fusedDecode\":%s,\"fusedDecode2560\":%s,"
+                     "\"fusedDecodeFault\":%lld}",
                      ctx->device, p.name, p.gcnArchName, p.multiProcessorCount, (unsigned long long)p.totalGlobalMem,
                      (unsigned long long)ctx->launches, (unsigned long long)ctx->allocated, ctx->buffers.size(),
                      (unsigned long long)ctx->bytes_written, (unsigned long long)ctx->bytes_read,
-                     ctx->fused_capable ? "true" : "false", faults);
+                     ctx->fused_capable ? "true" : "false", ctx->fused_capable_rg ? "true" : "false", faults);
     return n;
 }
 

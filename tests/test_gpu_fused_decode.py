@@ -1,4 +1,5 @@
-"""The single-launch decode layer (one token, hidden 2048 / ff 512) against
+"""The single-launch decode layer (one token, hidden 2048 / ff 512, and the
+real model's hidden 2560 / ff 640) against
 the three-kernel decode path and the CPU oracle: the same bits as the three
 kernels (both compute every product and sum in the same order), routing
 bit-exact with the oracle, and no wait ever giving up (fusedDecodeFault 0)
@@ -33,8 +34,8 @@ def two_layers(backend):
         l.free()
 
 
-def run_layer(b, lay, X, Y, ids, w, ws, mask, block=False, Hout=None, E=wl.EXPERTS, K=wl.TOPK, bias=None):
-    W, F = wl.WIDTH, wl.FF
+def run_layer(b, lay, X, Y, ids, w, ws, mask, block=False, Hout=None, E=wl.EXPERTS, K=wl.TOPK, bias=None,
+              W=wl.WIDTH, F=wl.FF):
     b.stage_select(mask)
     try:
         if block:
@@ -213,4 +214,114 @@ def test_fused_give_up_reported_and_reset(backend, two_layers):
     # and again, from the three kernels' side: the same bits
     run_layer(b, lay, X, Y1, ids, w, ws, THREE_KERNELS)
     assert np.array_equal(bits(b.read(Y1)), bits(y0))
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+# The real model's geometry (src/model.js:4-6): hidden 2560, expert ff 640.
+RW, RF = 2560, 640
+
+
+@pytest.fixture(scope="module")
+def rg_layers(backend):
+    ls = [wl.DeviceLayer(backend, layer=l, width=RW, ff=RF, experts=wl.EXPERTS, base_seed=wl.BASE_SEED + 1)
+          for l in (2, 3)]
+    yield ls
+    for l in ls:
+        l.free()
+
+
+def test_fused_2560_enabled(backend):
+    assert backend.info()["fusedDecode2560"] is True
+
+
+@pytest.mark.parametrize("block", [False, True])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_fused_2560_matches_three_kernels(backend, rg_layers, block, seed):
+    b = backend
+    E, K = wl.EXPERTS, wl.TOPK
+    lay = rg_layers[seed % 2]
+    X = b.alloc(RW, zero=False)
+    b.synth_normal(X, RW, 700 + seed, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_block_workspace_bytes(1, RW, RF, E, K))
+    outs = []
+    for mask in (ALL, THREE_KERNELS):
+        Y, ids, w = b.alloc(RW), b.alloc(K, "i32"), b.alloc(K)
+        run_layer(b, lay, X, Y, ids, w, ws, mask, block=block, Hout=Y, W=RW, F=RF)
+        outs.append((b.read(Y), b.read(ids), b.read(w)))
+    (y0, i0, w0), (y1, i1, w1) = outs
+    assert np.array_equal(i0, i1)
+    assert np.array_equal(bits(w0), bits(w1))
+    assert np.all(np.isfinite(y0))
+    assert np.array_equal(bits(y0), bits(y1)), float(np.abs(y0 - y1).max())
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+def test_fused_2560_many_launches(backend, rg_layers):
+    # 48 launches back to back and replayed from a graph twice, each equal to
+    # the three-kernel result for its input.
+    b = backend
+    E, K = wl.EXPERTS, wl.TOPK
+    n = 48
+    xs = []
+    for i in range(n):
+        x = b.alloc(RW, zero=False)
+        b.synth_normal(x, RW, 1300 + i, wl.STREAM_INPUT, 1.0)
+        xs.append(x)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, RW, RF, E, K))
+    ref = []
+    for i in range(n):
+        Y, ids, w = b.alloc(RW), b.alloc(K, "i32"), b.alloc(K)
+        run_layer(b, rg_layers[i % 2], xs[i], Y, ids, w, ws, THREE_KERNELS, W=RW, F=RF)
+        ref.append((b.read(Y), b.read(ids)))
+    outs = [(b.alloc(RW), b.alloc(K, "i32"), b.alloc(K)) for _ in range(n)]
+
+    def sequence():
+        for i in range(n):
+            run_layer(b, rg_layers[i % 2], xs[i], *outs[i], ws, ALL, W=RW, F=RF)
+
+    def check(tag):
+        for i in range(n):
+            assert np.array_equal(bits(b.read(outs[i][0])), bits(ref[i][0])), (tag, i)
+            assert np.array_equal(b.read(outs[i][1]), ref[i][1]), (tag, i)
+        for o in outs:
+            b.zero(o[0])
+
+    sequence()
+    check("eager")
+    b.graph_begin()
+    sequence()
+    gid = b.graph_end()
+    for rep in range(2):
+        b.graph_launch(gid)
+        b.sync()
+        check("replay %d" % rep)
+    b.graph_free(gid)
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+@pytest.mark.parametrize("experts,topk", [(512, 4), (300, 10), (130, 7)])
+def test_fused_2560_other_routing_shapes(backend, oracle, experts, topk):
+    # Fewer experts and smaller top-k at the real geometry (hidden rows past
+    # topk x 640 and down products of absent slots idle), against the oracle
+    # and the three kernels.
+    b = backend
+    lay = wl.DeviceLayer(b, layer=9, width=RW, ff=RF, experts=experts, base_seed=wl.BASE_SEED + 1)
+    X = b.alloc(RW, zero=False)
+    b.synth_normal(X, RW, 4100 + experts + topk, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, RW, RF, experts, topk))
+    Y, ids, w = b.alloc(RW), b.alloc(topk, "i32"), b.alloc(topk)
+    Y3, ids3, w3 = b.alloc(RW), b.alloc(topk, "i32"), b.alloc(topk)
+    run_layer(b, lay, X, Y, ids, w, ws, ALL, E=experts, K=topk, W=RW, F=RF)
+    run_layer(b, lay, X, Y3, ids3, w3, ws, THREE_KERNELS, E=experts, K=topk, W=RW, F=RF)
+    got_ids = b.read(ids)
+    host = wl.host_layer(oracle, 9, width=RW, ff=RF, experts=experts, base_seed=wl.BASE_SEED + 1,
+                         expert_ids=list(got_ids))
+    eY, eids, ew = oracle.moe_layer(b.read(X), 1, host["Wr"], host["arena"], host["stride"], host["shared"],
+                                    host["Wsg"], RW, RF, experts, topk)
+    lay.free()
+    assert np.array_equal(got_ids, eids)
+    assert np.array_equal(bits(b.read(w)), bits(ew))
+    got = b.read(Y)
+    assert tol_ok(got, eY), float(np.abs(got - eY).max())
+    assert np.array_equal(bits(got), bits(b.read(Y3)))
     assert b.info()["fusedDecodeFault"] == 0

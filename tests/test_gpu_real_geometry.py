@@ -4,8 +4,9 @@ bytes) on the GPU against the CPU oracle: routed IDs bit-exact for every
 token, routing weights bit-exact below 512 tokens and within 1e-6 relative
 from there on (the certified batch router), outputs of every token within
 |a - e| <= 1e-4 + 1e-3 |e|. The same kernels run both geometries; these
-cases cover the decode kernels with and without a token dimension, the
-16-row tiles of small batches and the 64-row tiles of prompts."""
+cases cover the single-launch decode layer (T = 1), the decode kernels with a
+token dimension, the 16-row tiles of small batches and the 64-row tiles of
+prompts."""
 import numpy as np
 import pytest
 
