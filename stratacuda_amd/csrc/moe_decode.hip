@@ -1245,10 +1245,14 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
         __hip_atomic_store(a.sync + kFusedFlagsB + b, launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // The down codes of this block's 8 output rows for the wave's slots
     // (wave and wave + 8): in flight while the hidden rows come in.
-    // RG: the down codes of the thread's (slot, row, group) products
-    // p = tid, tid + 512, tid + 1024 (p < RG_PAIRS; slot p / 100, row
-    // (p / 10) % 10, group p % 10), clamped to the last product.
-    constexpr int DQ = RG ? (RG_PAIRS + 64 * kFusedWaves - 1) / (64 * kFusedWaves) : 2;
+    // RG: thread tid < 440 takes (slot, group) pair tid / 4 (slot
+    // pair / 10, group pair % 10) and rows rg_row0 .. + rg_rows - 1 of the
+    // block's 10 (3, 3, 2, 2 rows for tid % 4 = 0..3), so that it reads
+    // the group's hidden values and forms their sum once; the down codes of
+    // those rows (a row past the last reloads it).
+    constexpr int DQ = RG ? 3 : 2;
+    const int rg_pair = min(tid >> 2, (kFusedMaxTopk + 1) * GD - 1), rg_sub = tid & 3;
+    const int rg_row0 = rg_sub < 2 ? 3 * rg_sub : 6 + 2 * (rg_sub - 2), rg_rows = rg_sub < 2 ? 3 : 2;
     uint4 dc[DQ];
     uint32_t dsb[DQ];
     bool dok[DQ];
@@ -1256,10 +1260,9 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
     for (int q = 0; q < DQ; q++) {
         int s, row, grp;
         if constexpr (RG) {
-            const int p = min(tid + 64 * kFusedWaves * q, RG_PAIRS - 1);
-            s = min(p / (DR * GD), nslot - 1);
-            row = b * DR + (p / GD) % DR;
-            grp = p % GD;
+            s = min(rg_pair / GD, nslot - 1);
+            row = b * DR + rg_row0 + min(q, rg_rows - 1);
+            grp = rg_pair % GD;
         } else {
             s = min(wave + kFusedWaves * q, nslot - 1);
             row = drow;
@@ -1327,11 +1330,9 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int q = 0; q < DQ; q++) {
-            const int p = tid + 64 * kFusedWaves * q;
-            const int k = p / (DR * GD), grp = p % GD;
-            if (p < RG_PAIRS && k < nslot) {
+        {
+            const int k = rg_pair / GD, grp = rg_pair % GD;
+            if (tid < 4 * (kFusedMaxTopk + 1) * GD && k < nslot) {
                 float h[64];
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
@@ -1341,7 +1342,14 @@ __global__ void __launch_bounds__(64 * kFusedWaves, 1) k_decode_fused(FusedArgs 
                     h[4 * i + 2] = v.z;
                     h[4 * i + 3] = v.w;
                 }
-                s_red[p] = dok[q] ? sm::half_bits(dsb[q]) * (dot64_4(dc[q], h) - sum64(h)) : __builtin_nanf("");
+                const float hs = sum64(h);
+#pragma unroll
+                for (int q = 0; q < DQ; q++) {
+                    if (q < rg_rows) {
+                        const float v = dok[q] ? sm::half_bits(dsb[q]) * (dot64_4(dc[q], h) - hs) : __builtin_nanf("");
+                        s_red[(k * DR + rg_row0 + q) * GD + grp] = v;
+                    }
+                }
             }
         }
         __syncthreads();
