@@ -67,7 +67,7 @@ def layer_flops(W, F, E, K, T):
     return T * ((K + 1) * 3 * 2 * W * F + 2 * E * W)
 
 
-def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefill_reps=4):
+def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefill_reps=4, prefetch=True):
     """The real model's geometry (hidden 2560, expert ff 640, 512 experts,
     top-10 + shared, 1,382,400-byte Q2 blobs) through the same kernels:
     decode T=1 rotating through `layers` resident layers (HIP graphs), the
@@ -83,6 +83,8 @@ def real_model(be, wl, np, capture, replay, release, layers=16, steps=960, prefi
 
     def step(i):
         s, lay = slots[i], lays[i]
+        if prefetch:
+            be.prefetch_router(lays[(i + 1) % layers].Wr, E, W)
         be.moe_layer(s["x"], 1, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, s["y"], s["ids"],
                      s["w"], s["ws"])
 
@@ -659,6 +661,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="issue every step directly instead of replaying HIP graphs (for profilers)")
+    ap.add_argument("--no-prefetch-router", action="store_true",
+                    help="no next-layer router prefetch: by default each decode step names the next step's router "
+                         "matrix (sm_prefetch_router), which its launch pulls into L2")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="seconds of T=1 CPU decodes (split over the 8- and 4-thread runs)")
     ap.add_argument("--cpu-quick", action="store_true", help="CPU baseline: T=1 only (no full prefill layers)")
@@ -719,6 +724,10 @@ def main():
 
     def step(i):
         s, lay = slots[i], layers[i]
+        if not args.no_prefetch_router:
+            # the router matrix of the step after this one (the next layer of
+            # the rotation), pulled into L2 by this step's launch
+            be.prefetch_router(layers[(i + 1) % L].Wr, E, W)
         be.moe_layer(s["x"], 1, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, F, E, K, s["y"], s["ids"],
                      s["w"], s["ws"])
 
@@ -920,7 +929,7 @@ def main():
         stack = {}
         blob = 2 * F * W // 4 + W * F // 4 + 2 * F * (W // 64) * 2 + W * (F // 64) * 2
         for T in (1, 32):
-            st = wl.DeviceStack(be, layers=layers, tokens=T, trace=True)
+            st = wl.DeviceStack(be, layers=layers, tokens=T, trace=True, prefetch=not args.no_prefetch_router)
             S = args.stack_steps
             inputs = be.alloc(S * T * W, zero=False)
             be.synth_normal(inputs, S * T * W, wl.BASE_SEED + 31 * T, wl.STREAM_INPUT, 1.0)
@@ -1003,6 +1012,9 @@ def main():
         "config": {"workload": "single MoE layer decode, T=1: hidden 2048, 512 experts, top-10 + shared, Q2 "
                                "(64-weight fp16-scale groups), 48 resident layers rotated per step",
                    "tokens_per_step": 1, "layers_rotated": L,
+                   "router_prefetch": ("each step names the next step's router matrix; its launch pulls those rows "
+                                       "into L2 while it waits (sm_prefetch_router)" if not args.no_prefetch_router
+                                       else None),
                    "execution": "HIP graph of 48 steps, one launch per step (k_decode_fused)" if fused else
                                 "HIP graph of 48 steps, three launches per step",
                    "gpu_us_per_step": round(gpu_ms * 1e3 / args.steps, 3),
@@ -1028,7 +1040,8 @@ def main():
             key = "prefill" if i == 0 else "prefill_" + case.replace("=", "").replace(" ", "_")
             out[key] = flat_prefill(case, r, W, F, E, K)
     for flag, name, fn in ((args.no_stack, "stack", section_stack),
-                           (args.no_real, "real_model", lambda: real_model(be, wl, np, capture, replay, release)),
+                           (args.no_real, "real_model",
+                            lambda: real_model(be, wl, np, capture, replay, release, prefetch=not args.no_prefetch_router)),
                            (args.no_dense, "dense_formats", lambda: dense_formats(be, np, capture, replay, release)),
                            (args.no_pack, "pack_load", section_pack), (args.no_prompt, "prompt", section_prompt)):
         out[name] = None

@@ -89,6 +89,18 @@ int sm_fused_fits(int compute_units, int blocks_per_cu);
 int sm_fused_reset(sm_ctx *ctx);
 int sm_fused_test_hooks(sm_ctx *ctx, uint32_t spin_limit, int withhold);
 
+/* Next-layer router prefetch, a hint for the next layer call (sm_moe_layer,
+ * sm_moe_block, sm_moe_layer_static) only: `Wr` (rows x width f32, 0 for
+ * none) is the router matrix of the call after that one. When the next call
+ * is a single-launch decode layer (one token), its blocks pull those rows
+ * into the GPU's L2 caches while they wait for each other, so that the
+ * following layer reads its router rows from L2 instead of HBM (each block's
+ * rows on the XCD where the next launch's block of the same index reads
+ * them). Any layer call clears the hint; a hint whose buffer is no longer
+ * live is dropped. Results never change. No counterpart in the reference
+ * (its engine prefetches expert blobs ahead of use, src/engine.js:144). */
+int sm_prefetch_router(sm_ctx *ctx, uint64_t Wr, int rows, int width);
+
 /* ---------------------------------------------------------------- buffers */
 /* zero != 0 clears the new buffer; refused (SM_E_ARG) while a graph is being
  * captured. sm_zero while capturing records a fill kernel, not a memset, and

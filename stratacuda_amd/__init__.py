@@ -89,6 +89,7 @@ def lib():
             "sm_moe_route_stats": (i, [vp, u64, i, i, i, i, i, pu64, ctypes.POINTER(i)]),
             "sm_fused_reset": (i, [vp]),
             "sm_fused_test_hooks": (i, [vp, ctypes.c_uint32, i]),
+            "sm_prefetch_router": (i, [vp, ctypes.c_uint64, i, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -233,6 +234,12 @@ class Backend:
     def fused_reset(self):
         """Clears the single-launch decode layer's fault (sm_fused_reset)."""
         self._check(lib().sm_fused_reset(self._ctx))
+
+    def prefetch_router(self, Wr, rows=0, width=0):
+        """The router matrix of the layer after the next one, pulled into L2
+        by the next single-launch decode layer (sm_prefetch_router); None
+        clears the hint."""
+        self._check(lib().sm_prefetch_router(self._ctx, Wr.handle if Wr is not None else 0, rows, width))
 
     def fused_test_hooks(self, spin_limit=0, withhold=False):
         """Test hook of the give-up path: poll limit (0 = default) and a collector

@@ -524,6 +524,18 @@ napi_value FusedReset(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// prefetchRouter(ctx, Wr, rows, width): the router matrix of the layer call
+// after the next one (0: none), pulled into L2 by the next single-launch decode layer
+napi_value PrefetchRouter(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!a.need(4)) return nullptr;
+    sm_ctx *ctx = a.ctx(0);
+    uint64_t Wr = a.u64(1);
+    int rows = a.i32(2), width = a.i32(3);
+    if (!a.ok || fail(env, ctx, sm_prefetch_router(ctx, Wr, rows, width))) return nullptr;
+    return undefined(env);
+}
+
 napi_value ModuleInit(napi_env env, napi_value exports) {
     struct Fn {
         const char *name;
@@ -559,7 +571,8 @@ napi_value ModuleInit(napi_env env, napi_value exports) {
                {"graphEnd", GraphEnd},
                {"graphLaunch", GraphLaunch},
                {"graphFree", GraphFree},
-               {"fusedReset", FusedReset}};
+               {"fusedReset", FusedReset},
+               {"prefetchRouter", PrefetchRouter}};
     for (const Fn &f : fns) {
         napi_value fn;
         napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);

@@ -60,6 +60,10 @@ struct sm_ctx {
     bool fused_capable_rg = false;  // hidden 2560 / ff 640
     uint32_t fused_spin_limit = 0, fused_withhold = 0;
     uint32_t *fault_host = nullptr, *fault_dev = nullptr;  // host pointer, and its device address
+    // sm_prefetch_router: the router matrix of the layer call after the next
+    // one (consumed by the next single-launch decode layer)
+    uint64_t next_wr = 0;
+    int next_rows = 0, next_width = 0;
     // Captured graphs kept beside their executables until sm_graph_free.
     std::vector<hipGraph_t> graph_sources;
 };

@@ -31,6 +31,19 @@ int need(sm_ctx *ctx, uint64_t handle, uint64_t bytes, const char *what) {
     return SM_OK;
 }
 
+// A layer call's use of the router-prefetch hint (sm_prefetch_router): kept
+// only while its buffer is still a live buffer of this context holding the
+// named rows; cleared once the call is issued (a hint serves one call).
+static void check_prefetch(sm_ctx *ctx) {
+    if (!ctx->next_wr) return;
+    auto it = ctx->buffers.find(ctx->next_wr);
+    if (it == ctx->buffers.end() || it->second < (uint64_t)ctx->next_rows * ctx->next_width * 4) ctx->next_wr = 0;
+}
+static int clear_prefetch(sm_ctx *ctx, int rc) {
+    ctx->next_wr = 0;
+    return rc;
+}
+
 int launched(sm_ctx *ctx) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return hip_fail(ctx, err, "kernel launch");
@@ -224,6 +237,19 @@ int sm_fused_reset(sm_ctx *ctx) {
                                 ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     *(volatile uint32_t *)ctx->fault_host = 0;
+    return SM_OK;
+}
+
+int sm_prefetch_router(sm_ctx *ctx, uint64_t Wr, int rows, int width) {
+    if (!ctx) return SM_E_ARG;
+    if (Wr && (rows <= 0 || rows > 4096 || width <= 0 || width % 64 != 0 || width > 8192))
+        return fail(ctx, SM_E_ARG, "prefetch: 1-4096 rows and a width that is a multiple of 64 up to 8192");
+    if (Wr) {
+        if (int rc = need(ctx, Wr, (uint64_t)rows * (uint64_t)width * 4, "prefetch router")) return rc;
+    }
+    ctx->next_wr = Wr;
+    ctx->next_rows = rows;
+    ctx->next_width = width;
     return SM_OK;
 }
 
@@ -487,11 +513,12 @@ int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps,
     if (Hout != H && Hout < H + (uint64_t)tokens * width * 4 && H < Hout + (uint64_t)tokens * width * 4)
         return fail(ctx, SM_E_ARG, "Hout must be H itself or not overlap it");
     const BlockArgs block = {gamma, eps};
+    check_prefetch(ctx);
     if (tokens <= kDecodeMaxTokens)
-        return moe_decode(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout, ids,
-                          weights, workspace, workspace_bytes, &block);
-    return moe_prefill(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Hout,
-                       ids, weights, workspace, workspace_bytes, &block);
+        return clear_prefetch(ctx, moe_decode(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
+                                              experts, topk, Hout, ids, weights, workspace, workspace_bytes, &block));
+    return clear_prefetch(ctx, moe_prefill(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
+                                           experts, topk, Hout, ids, weights, workspace, workspace_bytes, &block));
 }
 
 int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes) {
@@ -558,8 +585,9 @@ int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64
         if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
     if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
     if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
-    return moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
-                      weights, (uint64_t)ctx->scratch, kStaticScratchBytes);
+    check_prefetch(ctx);
+    return clear_prefetch(ctx, moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
+                                          experts, topk, Y, ids, weights, (uint64_t)ctx->scratch, kStaticScratchBytes));
 }
 
 int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,
@@ -584,11 +612,12 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
                               : moe_prefill_workspace(tokens, width, ff, experts, topk);
     if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
     if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
+    check_prefetch(ctx);
     if (tokens <= kDecodeMaxTokens)
-        return moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
-                          weights, workspace, workspace_bytes);
-    return moe_prefill(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y, ids,
-                       weights, workspace, workspace_bytes);
+        return clear_prefetch(ctx, moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
+                                              experts, topk, Y, ids, weights, workspace, workspace_bytes));
+    return clear_prefetch(ctx, moe_prefill(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
+                                           experts, topk, Y, ids, weights, workspace, workspace_bytes));
 }
 
 }  // extern "C"

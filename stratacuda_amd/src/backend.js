@@ -186,6 +186,14 @@ export class HipBackend {
         this.addon.fusedReset(this.ctx);
         if (this.failure && this.failure.code === 'SM_E_FAULT') this.failure = null;
     }
+    // The router matrix (rows x width f32) of the layer after the next one:
+    // the next single-launch decode layer pulls it into L2 (a hint for that
+    // one layer call; null clears it).
+    prefetchRouter(buffer, rows, width) {
+        this.assertAlive();
+        if (buffer === null) return this.addon.prefetchRouter(this.ctx, 0, 0, 0);
+        this.addon.prefetchRouter(this.ctx, this.owned(buffer, 'prefetch'), rows, width);
+    }
     // Bytes [offset, offset + bytes) of a buffer as an ArrayBuffer.
     async readBytes(buffer, offset, bytes) {
         this.assertAlive();

@@ -125,13 +125,16 @@ class DeviceStack:
     ``trace`` keeps every layer's input and routing for checking."""
 
     def __init__(self, backend, layers=48, tokens=1, width=WIDTH, ff=FF, experts=EXPERTS, topk=TOPK,
-                 base_seed=BASE_SEED, trace=False, fused=True):
+                 base_seed=BASE_SEED, trace=False, fused=True, prefetch=False):
         """``layers``: a count, or a list of existing DeviceLayer objects
         (layer l of the list is layer l of the stack; not freed here).
         ``fused``: one sm_moe_block call per layer (normalisation and
         residual folded into the stage's kernels) instead of the three
-        separate steps; the results are the same bits."""
-        self.b, self.T, self.fused = backend, tokens, fused
+        separate steps; the results are the same bits. ``prefetch``: each
+        layer call names the next layer's router matrix (the first layer's
+        after the last: the next step's), which a single-launch decode layer
+        pulls into L2 (sm_prefetch_router); the same bits."""
+        self.b, self.T, self.fused, self.prefetch = backend, tokens, fused, prefetch
         self.width, self.ff, self.experts, self.topk = width, ff, experts, topk
         self.own_layers = not isinstance(layers, list)
         self.layers = ([DeviceLayer(backend, l, width, ff, experts, base_seed) for l in range(layers)]
@@ -157,6 +160,8 @@ class DeviceStack:
             h_in = self.H[l if self.trace else l % 2]
             h_out = self.H[l + 1 if self.trace else (l + 1) % 2]
             ids, w = self.ids[l if self.trace else 0], self.w[l if self.trace else 0]
+            if self.prefetch:
+                b.prefetch_router(self.layers[(l + 1) % self.L].Wr, self.experts, W)
             if self.fused:
                 b.moe_block(h_in, T, lay.gamma, 1e-6, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, W, self.ff,
                             self.experts, self.topk, h_out, ids, w, self.ws)

@@ -24,7 +24,7 @@ test('the addon exports every entry of the C ABI it wraps', () => {
         'sync', 'kernels', 'signature', 'run', 'moeWorkspace', 'moeLayer', 'moeBlockWorkspace', 'moeBlock', 'moeRoute',
         'moeDispatch', 'synthNormal',
         'synthUniformPm', 'synthBlobs', 'eventRecord', 'eventElapsed', 'graphBegin', 'graphEnd', 'graphLaunch',
-        'graphFree', 'fusedReset'])
+        'graphFree', 'fusedReset', 'prefetchRouter'])
         assert.strictEqual(typeof real[f], 'function', f);
     assert.ok(real.kernels().indexOf('strata_router') >= 0);
     assert.strictEqual(real.signature('strata_router'), 'Logits:f32*,Ids:i32*,Weights:f32*,experts:i32,topK:i32');
@@ -209,6 +209,19 @@ test('a fused decode fault fails read() and idle() until resetFusedDecode()', as
     b.resetFusedDecode();
     assert.strictEqual(resets, 1);
     assert.deepStrictEqual(Array.from(await b.read(y)), [1, 2]);
+    await b.idle();
+});
+
+test('prefetchRouter passes an owned buffer, rejects foreign ones and clears with null', async () => {
+    const addon = fakeAddon();
+    const calls = [];
+    addon.prefetchRouter = (...a) => calls.push(a.slice(1));
+    const b = await HipBackend.create({addon});
+    const wr = b.alloc(512 * 64);
+    b.prefetchRouter(wr, 512, 64);
+    b.prefetchRouter(null);
+    assert.deepStrictEqual(calls, [[wr.id, 512, 64], [0, 0, 0]]);
+    assert.throws(() => b.prefetchRouter({id: 1, byteLength: 4}, 1, 64), /Invalid HIP prefetch/);
     await b.idle();
 });
 

@@ -325,3 +325,65 @@ def test_fused_2560_other_routing_shapes(backend, oracle, experts, topk):
     assert tol_ok(got, eY), float(np.abs(got - eY).max())
     assert np.array_equal(bits(got), bits(b.read(Y3)))
     assert b.info()["fusedDecodeFault"] == 0
+
+
+@pytest.mark.parametrize("geometry", ["2048", "2560"])
+def test_router_prefetch_changes_no_bits(backend, two_layers, rg_layers, geometry):
+    # Each step names the next step's router matrix (sm_prefetch_router), so
+    # the single launch pulls it into L2 while it waits: eager and replayed
+    # from a graph, the bits equal those of the same steps without hints. A
+    # hint whose buffer was freed before the call is dropped.
+    b = backend
+    E, K = wl.EXPERTS, wl.TOPK
+    W, F, lays = (wl.WIDTH, wl.FF, two_layers) if geometry == "2048" else (RW, RF, rg_layers)
+    n = 8
+    xs = []
+    for i in range(n):
+        x = b.alloc(W, zero=False)
+        b.synth_normal(x, W, 2100 + i, wl.STREAM_INPUT, 1.0)
+        xs.append(x)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, W, F, E, K))
+    outs = [(b.alloc(W), b.alloc(K, "i32"), b.alloc(K)) for _ in range(n)]
+
+    def sequence(hint):
+        for i in range(n):
+            if hint:
+                b.prefetch_router(lays[(i + 1) % 2].Wr, E, W)
+            run_layer(b, lays[i % 2], xs[i], *outs[i], ws, ALL, W=W, F=F)
+
+    sequence(False)
+    ref = [(bits(b.read(o[0])), b.read(o[1])) for o in outs]
+
+    def check(tag):
+        for i in range(n):
+            assert np.array_equal(bits(b.read(outs[i][0])), ref[i][0]), (tag, i)
+            assert np.array_equal(b.read(outs[i][1]), ref[i][1]), (tag, i)
+            b.zero(outs[i][0])
+
+    sequence(True)
+    check("eager")
+    b.graph_begin()
+    sequence(True)
+    gid = b.graph_end()
+    for rep in range(2):
+        b.graph_launch(gid)
+        b.sync()
+        check("replay %d" % rep)
+    b.graph_free(gid)
+    gone = b.alloc(E * W, zero=True)
+    b.prefetch_router(gone, E, W)
+    b.free(gone)
+    run_layer(b, lays[0], xs[0], *outs[0], ws, ALL, W=W, F=F)
+    assert np.array_equal(bits(b.read(outs[0][0])), ref[0][0])
+    assert b.info()["fusedDecodeFault"] == 0
+
+
+def test_router_prefetch_rejects_bad_hints(backend, two_layers):
+    b = backend
+    with pytest.raises(sm.ArgumentError):
+        b.prefetch_router(two_layers[0].Wr, 0, wl.WIDTH)
+    with pytest.raises(sm.ArgumentError):
+        b.prefetch_router(two_layers[0].Wr, wl.EXPERTS, 100)
+    with pytest.raises(sm.StrataError):
+        b.prefetch_router(two_layers[0].Wr, wl.EXPERTS * 2, wl.WIDTH)  # more rows than the buffer holds
+    b.prefetch_router(None)
