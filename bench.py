@@ -842,7 +842,10 @@ def main():
         dk = three[dom]
     roofline = {"bound": "hbm", "kernel": hip_kernel, "achieved": dk["GB/s"], "peak": PEAK_HBM / 1e9,
                 "unit": "GB/s", "frac": dk["frac_hbm"], "traffic": read_traffic(hip_kernel),
-                "bytes_per_launch": dk["bytes_per_launch"], "avg_us": dk["avg_us"]}
+                "bytes_per_launch": dk["bytes_per_launch"], "avg_us": dk["avg_us"],
+                "traffic_source": "profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per launch, copy-kernel calibrated, "
+                                  "measured without the next-layer router prefetch (with it a launch also fetches "
+                                  "the next layer's W_r into L2; profiles/traffic_decode_T1.md)"}
     # whole step against the per-token algorithmic bytes
     step_s = gpu_ms * 1e-3 / args.steps
     layer_roof = {"bound": "hbm", "bytes_per_step": step_bytes, "achieved": round(step_bytes / step_s / 1e9, 1),
