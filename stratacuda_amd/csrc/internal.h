@@ -27,6 +27,9 @@ struct sm_ctx {
     // loader's and the index checks' flags; from kFusedSyncBase the fused
     // decode layer's hand-off counters, go words and sticky fault word.
     uint32_t *counters = nullptr;
+    // Scores of the batched prompt attention (strata_attention_batch):
+    // tokens x heads x 2,048 cells, kAttnScoresBytes, allocated by sm_init.
+    float *attn_scores = nullptr;
     uint64_t launches = 0, bytes_written = 0, bytes_read = 0, allocated = 0;
     // Stage timing (sm_stage_timing): events recorded at stage boundaries.
     bool stage_timing = false;
@@ -188,6 +191,8 @@ uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int to
 constexpr uint64_t kStaticScratchBytes = 2ull << 20;
 constexpr int kMaxDevices = 64;
 int static_scratch_init(sm_ctx *ctx);
+// Size of ctx->attn_scores: 1,024 (token, head) rows of 2,048 cells.
+constexpr uint64_t kAttnScoresBytes = 1024ull * 2048 * 4;
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
                 uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff, int experts,
                 int topk, uint64_t Y, uint64_t ids, uint64_t weights, uint64_t workspace,

@@ -528,6 +528,248 @@ __global__ __launch_bounds__(256) void k_attention_batch4(const float *__restric
     Y[(int64_t)(token * heads + h) * dim + d] = value / total;
 }
 
+// The batched prompt attention in two launches, the same operations in the
+// same order as k_attention_batch4 (kernels/strata.cu:512-534), with the
+// work spread over the GPU:
+//  k_attn_scores: one block per (64-cell tile, KV head, token). The tile's
+//    keys (64 rows) go to LDS with 16-byte loads, the query rows of the KV
+//    head's query heads too; lane l of wave w forms cell c0 + l's score for
+//    query heads w, w + 4, ... (HPW of them side by side, each the
+//    sequential dot over the head dimension), times `scale`, into
+//    S[token][head][cell].
+//  k_attn_values: below.
+// A row of keys in LDS is padded by 4 floats so that the 64 lanes' 16-byte
+// reads of one offset spread over the banks.
+template <int D, int HPW>
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ Q, const float *__restrict__ Keys,
+                                                     float *__restrict__ S, int heads, int kvHeads, int position,
+                                                     float scale, int hu) {
+    constexpr int P = D + 4;
+    __shared__ __attribute__((aligned(16))) float s_k[64 * P];
+    __shared__ __attribute__((aligned(16))) float s_q[4 * HPW][D];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int token = blockIdx.z, kh = blockIdx.y, c0 = blockIdx.x * 64, count = position + token + 1;
+    if (c0 >= count) return;
+    const int group = heads / kvHeads, h0 = kh * group;
+    for (int idx = tid; idx < 64 * (D / 4); idx += 256) {
+        const int r = idx / (D / 4), i4 = idx - r * (D / 4), cell = min(c0 + r, count - 1);
+        *(float4 *)&s_k[r * P + 4 * i4] = ((const float4 *)(Keys + ((int64_t)cell * kvHeads + kh) * D))[i4];
+    }
+    for (int idx = tid; idx < group * (D / 4); idx += 256) {
+        const int g = idx / (D / 4), i4 = idx - g * (D / 4);
+        *(float4 *)&s_q[g][4 * i4] = ((const float4 *)(Q + ((int64_t)token * heads + h0 + g) * D))[i4];
+    }
+    __syncthreads();
+    float score[HPW];
+#pragma unroll
+    for (int u = 0; u < HPW; u++) score[u] = 0.0f;
+    const float *kr = &s_k[lane * P];
+    for (int j = 0; j < D; j += 4) {
+        const float4 k4 = *(const float4 *)&kr[j];
+#pragma unroll
+        for (int u = 0; u < HPW; u++) {
+            const int g = min(w + 4 * u, group - 1);
+            const float4 q4 = *(const float4 *)&s_q[g][j];
+            float v = score[u];
+            v = v + q4.x * k4.x;
+            v = v + q4.y * k4.y;
+            v = v + q4.z * k4.z;
+            v = v + q4.w * k4.w;
+            score[u] = v;
+        }
+    }
+    const int cell = c0 + lane;
+#pragma unroll
+    for (int u = 0; u < HPW; u++) {
+        const int g = w + 4 * u, h = h0 + g;
+        if (g < group && h < hu && cell < count) S[((int64_t)token * heads + h) * 2048 + cell] = score[u] * scale;
+    }
+}
+
+// k_attn_values: one block per (64-component tile, group of up to HPW query
+// heads of one KV head, token); wave w handles head w of the group. First
+// the reference's softmax of its scores: the maximum, the exponentials and
+// their sum in the reference's lane order (lane l: cells l, l + 64, ...; the
+// tree), the probabilities in LDS. Then the weighted sum over the cells of
+// the tile's 64 components: the block's waves share the values, staged
+// through LDS 16 HPW cells at a time by all threads (double-buffered: the
+// next chunk's loads are in flight while this one is summed, and the
+// barriers order LDS only, so they do not wait for them); each lane's sum
+// runs over the cells in order.
+template <int D, int HPW>
+__global__ __launch_bounds__(64 * HPW) void k_attn_values(const float *__restrict__ S, const float *__restrict__ Values,
+                                                         float *__restrict__ Y, int heads, int kvHeads, int position,
+                                                         int hu, int tiles) {
+    constexpr int CH = 16 * HPW;  // cells per chunk: four 16-byte loads per thread
+    __shared__ __attribute__((aligned(16))) float s_p[HPW][2048];
+    __shared__ __attribute__((aligned(16))) float s_v[2][CH][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int token = blockIdx.z, count = position + token + 1, group = heads / kvHeads;
+    const int groups_per_kv = (group + HPW - 1) / HPW;
+    const int kh = blockIdx.y / groups_per_kv, g = (blockIdx.y - kh * groups_per_kv) * HPW + w;
+    const int h = kh * group + g;
+    const bool live = g < group && h < hu;
+    // (all 32 of the lane's scores loaded at once, clamped past the count)
+    const float *sc = S + ((int64_t)token * heads + min(h, heads - 1)) * 2048;
+    float sv[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) sv[i] = sc[min(lane + 64 * i, count - 1)];
+    float mx = kNegBig;
+#pragma unroll
+    for (int i = 0; i < 32; i++)
+        if (lane + 64 * i < count) mx = fmaxf(mx, sv[i]);
+    for (int s = 32; s > 0; s >>= 1) mx = fmaxf(mx, __shfl_down(mx, s, 64));
+    mx = __shfl(mx, 0, 64);
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        if (lane + 64 * i < count) {
+            const float p = sm::expf_or(sv[i] - mx);
+            s_p[w][lane + 64 * i] = p;
+            sum = sum + p;
+        }
+    }
+    const float total = __shfl(sm::tree_sum64(sum), 0, 64);
+    const int d = blockIdx.x * 64 + lane;
+    const int64_t vstride = (int64_t)kvHeads * D;
+    const float *vtile = Values + (int64_t)kh * D + blockIdx.x * 64;
+    const int nch = (count + CH - 1) / CH;
+    // (four named registers, not an array: the compiler can place a small
+    // private array in LDS, and then waits for the loads at once)
+    const int row = threadIdx.x / 16, col = 4 * (threadIdx.x & 15);  // 16 threads per cell row
+    constexpr int RS = 4 * HPW;  // cell rows between a thread's four loads
+    auto vload = [&](int cell) -> float4 {
+        return *(const float4 *)(vtile + (int64_t)min(cell, count - 1) * vstride + col);
+    };
+    float4 l0 = vload(row), l1 = vload(row + RS), l2 = vload(row + 2 * RS), l3 = vload(row + 3 * RS);
+    *(float4 *)&s_v[0][row][col] = l0;
+    *(float4 *)&s_v[0][row + RS][col] = l1;
+    *(float4 *)&s_v[0][row + 2 * RS][col] = l2;
+    *(float4 *)&s_v[0][row + 3 * RS][col] = l3;
+    float value = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        if (c + 1 < nch) {
+            const int c1 = (c + 1) * CH + row;
+            l0 = vload(c1);
+            l1 = vload(c1 + RS);
+            l2 = vload(c1 + 2 * RS);
+            l3 = vload(c1 + 3 * RS);
+        }
+        // (the next chunk's loads are issued here, not sunk to their use)
+        asm volatile("" ::: "memory");
+        sm::lds_barrier();  // chunk c is in LDS (and the probabilities); chunk c - 1's buffer is free
+        const int t0 = c * CH, n = min(CH, count - t0), buf = c & 1;
+        // 16 cells at a time: their values and probabilities read from LDS
+        // into registers, then the 16 steps of the sum
+        for (int gg = 0; gg < n; gg += 16) {
+            float vv[16], pp[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) vv[u] = s_v[buf][min(gg + u, CH - 1)][lane];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 p4 = *(const float4 *)&s_p[w][min(t0 + gg + 4 * i, 2044)];
+                pp[4 * i] = p4.x;
+                pp[4 * i + 1] = p4.y;
+                pp[4 * i + 2] = p4.z;
+                pp[4 * i + 3] = p4.w;
+            }
+            if (gg + 16 <= n) {
+#pragma unroll
+                for (int u = 0; u < 16; u++) value = value + pp[u] * vv[u];
+            } else {
+                for (int u = 0; u < n - gg; u++) {
+                    float a = pp[0], b = vv[0];
+#pragma unroll
+                    for (int i = 1; i < 16; i++) {
+                        a = u == i ? pp[i] : a;
+                        b = u == i ? vv[i] : b;
+                    }
+                    value = value + a * b;
+                }
+            }
+        }
+        // the next chunk goes to LDS only after this one is summed (its loads
+        // were in flight meanwhile)
+        asm volatile("" ::: "memory");
+        if (c + 1 < nch) {
+            const int nb = (c + 1) & 1;
+            *(float4 *)&s_v[nb][row][col] = l0;
+            *(float4 *)&s_v[nb][row + RS][col] = l1;
+            *(float4 *)&s_v[nb][row + 2 * RS][col] = l2;
+            *(float4 *)&s_v[nb][row + 3 * RS][col] = l3;
+        }
+    }
+    if (live && blockIdx.x < (unsigned)tiles && d < D) Y[((int64_t)token * heads + h) * D + d] = value / total;
+}
+
+// k_gdn_batch_reg with the key and query rows of the block's key head staged
+// in LDS (16 tokens at a time) and one 64-thread block per 64 state columns
+// (all of one value head: D is a multiple of 64), so that each of the
+// column's two sequential sums per token reads its K / Q values from LDS
+// instead of waiting on global loads, and the columns spread over the CUs.
+// Decay, Beta and V of the staged tokens are loaded with them. The same
+// operations in the same order as the reference (kernels/strata.cu:432-445).
+constexpr int kGdnStage = 16;
+template <int D>
+__global__ void __launch_bounds__(64) k_gdn_batch_lds(float *__restrict__ State, const float *__restrict__ Q,
+                                                      const float *__restrict__ K, const float *__restrict__ V,
+                                                      const float *__restrict__ Decay, const float *__restrict__ Beta,
+                                                      float *__restrict__ Y, int keyHeads, int valueHeads, int tokens,
+                                                      int n) {
+    static_assert(D % 64 == 0 && D <= GDN_REG_MAX_DIM, "whole value heads per block group");
+    __shared__ __attribute__((aligned(16))) float s_k[kGdnStage][D], s_q[kGdnStage][D];
+    __shared__ float s_decay[kGdnStage], s_beta[kGdnStage];
+    const int jh = blockIdx.x * 64 + threadIdx.x;
+    const int h = (int)(blockIdx.x * 64) / D, kh = h % keyHeads, stride = valueHeads * D;
+    const bool live = jh < n;
+    const int col = min(jh, n - 1);
+    float st[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) st[i] = State[(int64_t)i * stride + col];
+    for (int t0 = 0; t0 < tokens; t0 += kGdnStage) {
+        const int nt = min(kGdnStage, tokens - t0);
+        __syncthreads();  // the previous stage's readers are done
+        for (int idx = threadIdx.x; idx < nt * (D / 4); idx += 64) {
+            const int tt = idx / (D / 4), i4 = idx - tt * (D / 4);
+            const int64_t qbase = ((int64_t)(t0 + tt) * keyHeads + kh) * D;
+            *(float4 *)&s_k[tt][4 * i4] = ((const float4 *)(K + qbase))[i4];
+            *(float4 *)&s_q[tt][4 * i4] = ((const float4 *)(Q + qbase))[i4];
+        }
+        if (threadIdx.x < nt) {
+            s_decay[threadIdx.x] = Decay[(t0 + threadIdx.x) * valueHeads + h];
+            s_beta[threadIdx.x] = Beta[(t0 + threadIdx.x) * valueHeads + h];
+        }
+        float vv[kGdnStage];
+#pragma unroll
+        for (int tt = 0; tt < kGdnStage; tt++) vv[tt] = V[(int64_t)(t0 + min(tt, nt - 1)) * stride + col];
+        __syncthreads();
+        for (int tt = 0; tt < nt; tt++) {
+            const float decay = s_decay[tt];
+            float prediction = 0.0f;
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                st[i] = st[i] * decay;
+                prediction = prediction + st[i] * s_k[tt][i];
+            }
+            float vt = vv[0];
+#pragma unroll
+            for (int u = 1; u < kGdnStage; u++) vt = tt == u ? vv[u] : vt;
+            const float delta = (vt - prediction) * s_beta[tt];
+            float result = 0.0f;
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                st[i] = st[i] + s_k[tt][i] * delta;
+                result = result + st[i] * s_q[tt][i];
+            }
+            if (live) Y[(int64_t)(t0 + tt) * stride + jh] = result;
+        }
+    }
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) State[(int64_t)i * stride + jh] = st[i];
+    }
+}
+
 // ------------------------------------------------------------- launchers
 int bad(sm_ctx *ctx, const std::string &m) { return fail(ctx, SM_E_ARG, m); }
 unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -906,6 +1148,12 @@ int L_gdn_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
     // a State that no other argument aliases (the same handle twice).
     bool distinct = true;
     for (int i = 1; i < 7; i++) distinct = distinct && a.ptr(i) != a.ptr(0);
+    if (distinct && (dim == 64 || dim == 128)) {
+        // whole value heads of 64-column blocks, K / Q staged in LDS
+        (dim == 64 ? k_gdn_batch_lds<64> : k_gdn_batch_lds<128>)<<<(unsigned)((n + 63) / 64), 64, 0, ctx->stream>>>(
+            Fw(a, 0), F(a, 1), F(a, 2), F(a, 3), F(a, 4), F(a, 5), Fw(a, 6), keyHeads, valueHeads, tokens, (int)n);
+        return launched(ctx);
+    }
     (dim <= GDN_REG_MAX_DIM && distinct ? k_gdn_batch_reg : k_gdn_batch)<<<blocks256(n), 256, 0, ctx->stream>>>(
         Fw(a, 0), F(a, 1), F(a, 2), F(a, 3), F(a, 4), F(a, 5), Fw(a, 6), dim, keyHeads, valueHeads, tokens, (int)n);
     return launched(ctx);
@@ -981,6 +1229,31 @@ int L_attention_batch(sm_ctx *ctx, const uint32_t *G, Args a) {
     if (int rc = need(ctx, a.ptr(1), kv, "Keys")) return rc;
     if (int rc = need(ctx, a.ptr(2), kv, "Values")) return rc;
     if (int rc = need(ctx, a.ptr(3), (uint64_t)((int64_t)(tu - 1) * heads + hu) * dim * 4, "Y")) return rc;
+    // Two launches over the whole GPU (k_attn_scores, k_attn_values) for the
+    // production head sizes; one otherwise.
+    const int group = heads / kvHeads;
+    if ((dim == 64 || dim == 128 || dim == 256) && group <= 16 && (uint64_t)tu * heads * 2048 * 4 <= kAttnScoresBytes) {
+        using KS = void (*)(const float *, const float *, float *, int, int, int, float, int);
+        const int di = dim == 64 ? 0 : dim == 128 ? 1 : 2, hpw = (group + 3) / 4;
+        static const KS ks[3][4] = {{k_attn_scores<64, 1>, k_attn_scores<64, 2>, k_attn_scores<64, 3>, k_attn_scores<64, 4>},
+                                    {k_attn_scores<128, 1>, k_attn_scores<128, 2>, k_attn_scores<128, 3>,
+                                     k_attn_scores<128, 4>},
+                                    {k_attn_scores<256, 1>, k_attn_scores<256, 2>, k_attn_scores<256, 3>,
+                                     k_attn_scores<256, 4>}};
+        using KV = void (*)(const float *, const float *, float *, int, int, int, int, int);
+        const int vh = group >= 4 ? 4 : group >= 2 ? 2 : 1, vi = vh == 4 ? 2 : vh == 2 ? 1 : 0;
+        static const KV kv[3][3] = {{k_attn_values<64, 1>, k_attn_values<64, 2>, k_attn_values<64, 4>},
+                                    {k_attn_values<128, 1>, k_attn_values<128, 2>, k_attn_values<128, 4>},
+                                    {k_attn_values<256, 1>, k_attn_values<256, 2>, k_attn_values<256, 4>}};
+        const int kvu = std::min(kvHeads, (hu - 1) / group + 1), cells = position + tu;
+        ks[di][hpw - 1]<<<dim3((cells + 63) / 64, kvu, tu), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), ctx->attn_scores,
+                                                                                    heads, kvHeads, position, scale, hu);
+        if (int rc = launched(ctx)) return rc;
+        const int gpk = (group + vh - 1) / vh;
+        kv[di][vi]<<<dim3(tiles, kvu * gpk, tu), 64 * vh, 0, ctx->stream>>>(ctx->attn_scores, F(a, 2), Fw(a, 3), heads,
+                                                                            kvHeads, position, hu, tiles);
+        return launched(ctx);
+    }
     k_attention_batch4<<<dim3(hu, (tiles + 3) / 4, tu), 256, 0, ctx->stream>>>(F(a, 0), F(a, 1), F(a, 2), Fw(a, 3),
                                                                                  dim, heads, kvHeads, position, scale,
                                                                                  tiles);

@@ -144,6 +144,7 @@ int sm_init(int device, sm_ctx **out) {
         }
     }
     if (hipMalloc((void **)&ctx->counters, kCounterWords * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc((void **)&ctx->attn_scores, kAttnScoresBytes) != hipSuccess ||
         hipMemset(ctx->counters, 0, kCounterWords * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         sm_shutdown(ctx);
@@ -178,6 +179,7 @@ void sm_shutdown(sm_ctx *ctx) {
     for (auto &kv : ctx->buffers) (void)hipFree((void *)kv.first);
     ctx->buffers.clear();
     if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->attn_scores) (void)hipFree(ctx->attn_scores);
     pack_release(ctx);
     for (auto &e : ctx->stage_pool) (void)hipEventDestroy(e);
     for (auto &g : ctx->graphs)

@@ -73,7 +73,7 @@ def test_conv_batch_state_across_chunks(backend, oracle, channels, taps, dilatio
         same(backend.read(hb), hist)
 
 
-@pytest.mark.parametrize("dim,kh,vh,tokens", [(8, 2, 4, 5), (128, 16, 48, 4)])
+@pytest.mark.parametrize("dim,kh,vh,tokens", [(8, 2, 4, 5), (128, 16, 48, 4), (128, 16, 48, 21), (64, 2, 6, 3)])
 def test_gdn_gates_and_gdn_batch(backend, oracle, dim, kh, vh, tokens):
     rng = np.random.default_rng(dim * tokens)
     alpha = rng.normal(0, 3, vh * tokens).astype(np.float32)
@@ -146,7 +146,8 @@ def test_rope_batch(backend, oracle, dim, rotary, heads, tokens):
 
 
 @pytest.mark.parametrize("dim,heads,kvh,position,tokens", [(8, 4, 2, 1, 5), (70, 4, 2, 60, 7), (256, 24, 2, 0, 16),
-                                                           (256, 24, 2, 2032, 16), (128, 4, 4, 100, 64)])
+                                                           (256, 24, 2, 2032, 16), (128, 4, 4, 100, 64),
+                                                           (64, 12, 2, 500, 20)])
 def test_kv_append_attention_and_gate_batch(backend, oracle, dim, heads, kvh, position, tokens):
     rng = np.random.default_rng(position + tokens)
     width, cells = kvh * dim, position + tokens
