@@ -707,9 +707,16 @@ __global__ __launch_bounds__(64 * HPW) void k_attn_values(const float *__restric
 // (all of one value head: D is a multiple of 64), so that each of the
 // column's two sequential sums per token reads its K / Q values from LDS
 // instead of waiting on global loads, and the columns spread over the CUs.
-// Decay, Beta and V of the staged tokens are loaded with them. The same
-// operations in the same order as the reference (kernels/strata.cu:432-445).
+// The K / Q rows arrive by DMA, Decay and Beta of the staged tokens with
+// them, and each token's V value one token ahead. The same operations in the
+// same order as the reference (kernels/strata.cu:432-445). At the
+// production shape (6,144 columns: 96 waves) each wave runs two dependent
+// 128-step sums per token; the kernel is bound by that latency.
 constexpr int kGdnStage = 16;
+// 16 bytes per lane from global memory into LDS (lane l's at base + 16 l).
+__device__ __forceinline__ void gdn_dma16(const void *src, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
+}
 template <int D>
 __global__ void __launch_bounds__(64) k_gdn_batch_lds(float *__restrict__ State, const float *__restrict__ Q,
                                                       const float *__restrict__ K, const float *__restrict__ V,
@@ -729,21 +736,30 @@ __global__ void __launch_bounds__(64) k_gdn_batch_lds(float *__restrict__ State,
     for (int t0 = 0; t0 < tokens; t0 += kGdnStage) {
         const int nt = min(kGdnStage, tokens - t0);
         __syncthreads();  // the previous stage's readers are done
-        for (int idx = threadIdx.x; idx < nt * (D / 4); idx += 64) {
-            const int tt = idx / (D / 4), i4 = idx - tt * (D / 4);
-            const int64_t qbase = ((int64_t)(t0 + tt) * keyHeads + kh) * D;
-            *(float4 *)&s_k[tt][4 * i4] = ((const float4 *)(K + qbase))[i4];
-            *(float4 *)&s_q[tt][4 * i4] = ((const float4 *)(Q + qbase))[i4];
+        // K and Q rows of the stage's tokens by DMA into LDS (16 bytes per
+        // lane, a kilobyte per instruction: 1,024 / (4 D) rows; rows past
+        // the stage's tokens reload its last token and are never read)
+        constexpr int RPI = 256 / D;  // rows per instruction
+        const int lr = threadIdx.x / (D / 4), lo = 4 * (threadIdx.x % (D / 4));
+#pragma unroll
+        for (int i = 0; i < kGdnStage / RPI; i++) {
+            const int tt = min(RPI * i + lr, nt - 1);
+            const int64_t qbase = ((int64_t)(t0 + tt) * keyHeads + kh) * D + lo;
+            gdn_dma16(K + qbase, &s_k[RPI * i][0]);
+            gdn_dma16(Q + qbase, &s_q[RPI * i][0]);
         }
         if (threadIdx.x < nt) {
             s_decay[threadIdx.x] = Decay[(t0 + threadIdx.x) * valueHeads + h];
             s_beta[threadIdx.x] = Beta[(t0 + threadIdx.x) * valueHeads + h];
         }
-        float vv[kGdnStage];
-#pragma unroll
-        for (int tt = 0; tt < kGdnStage; tt++) vv[tt] = V[(int64_t)(t0 + min(tt, nt - 1)) * stride + col];
+        __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0): the DMA is in LDS
         __syncthreads();
+        // the token's V value, loaded one token ahead (one register, not a
+        // register per staged token)
+        float vnext = V[(int64_t)t0 * stride + col];
         for (int tt = 0; tt < nt; tt++) {
+            const float vt = vnext;
+            vnext = V[(int64_t)(t0 + min(tt + 1, nt - 1)) * stride + col];
             const float decay = s_decay[tt];
             float prediction = 0.0f;
 #pragma unroll
@@ -751,9 +767,6 @@ __global__ void __launch_bounds__(64) k_gdn_batch_lds(float *__restrict__ State,
                 st[i] = st[i] * decay;
                 prediction = prediction + st[i] * s_k[tt][i];
             }
-            float vt = vv[0];
-#pragma unroll
-            for (int u = 1; u < kGdnStage; u++) vt = tt == u ? vv[u] : vt;
             const float delta = (vt - prediction) * s_beta[tt];
             float result = 0.0f;
 #pragma unroll
