@@ -387,3 +387,32 @@ def test_router_prefetch_rejects_bad_hints(backend, two_layers):
     with pytest.raises(sm.StrataError):
         b.prefetch_router(two_layers[0].Wr, wl.EXPERTS * 2, wl.WIDTH)  # more rows than the buffer holds
     b.prefetch_router(None)
+
+
+def test_fused_2560_give_up_reported_and_reset(backend, rg_layers):
+    # The same forced give-up at the real geometry: NaN outputs, SM_E_FAULT
+    # from sync, bit-identical results after the reset.
+    b = backend
+    E, K = wl.EXPERTS, wl.TOPK
+    lay = rg_layers[0]
+    X = b.alloc(RW, zero=False)
+    b.synth_normal(X, RW, 37, wl.STREAM_INPUT, 1.0)
+    ws = b.alloc_bytes(b.moe_workspace_bytes(1, RW, RF, E, K))
+    ids, w = b.alloc(K, "i32"), b.alloc(K)
+    Y0, Y1, Y2 = (b.alloc(RW) for _ in range(3))
+    run_layer(b, lay, X, Y0, ids, w, ws, ALL, W=RW, F=RF)
+    y0 = b.read(Y0)
+    try:
+        b.fused_test_hooks(spin_limit=64, withhold=True)
+        print("fused 2560 give-up: withheld launch", flush=True)
+        run_layer(b, lay, X, Y1, ids, w, ws, ALL, W=RW, F=RF)
+        with pytest.raises(sm.StrataError) as err:
+            b.idle()
+        assert err.value.code == sm.SM_E_FAULT
+    finally:
+        b.fused_test_hooks()
+        b.fused_reset()
+    assert np.all(np.isnan(b.read(Y1)))
+    run_layer(b, lay, X, Y2, ids, w, ws, ALL, W=RW, F=RF)
+    assert np.array_equal(bits(b.read(Y2)), bits(y0))
+    assert b.info()["fusedDecodeFault"] == 0
