@@ -86,6 +86,45 @@ __global__ void __launch_bounds__(256) k_split_hilo(const float *__restrict__ X,
     *(half8 *)(out + rg * 128 + 64 + 8 * c) = lo;
 }
 
+// The stack block's RMSNorm for small batches (kernels/strata.cu strata_norm
+// mode 0, one gamma row, scale 1: the lane-strided sum of squares and its
+// tree, as k_norm_reg forms it, so the f32 rows are bit-identical) writing
+// the router's f32 input and, from the same registers, the hi/lo fp16 split
+// of k_split_hilo for the expert GEMMs. One wave per row of NJ x 64 values.
+template <int NJ>
+__global__ void __launch_bounds__(256) k_norm_hilo(const float *__restrict__ X, const float *__restrict__ gamma,
+                                                   float *__restrict__ Y, _Float16 *__restrict__ hl, int rows,
+                                                   float eps) {
+    const int row = (int)(blockIdx.x * 4 + (threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    constexpr int cols = NJ * 64;
+    const float *xr = X + (int64_t)row * cols;
+    float x[NJ], w[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) x[j] = xr[lane + 64 * j];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) w[j] = gamma[lane + 64 * j];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) ss = ss + x[j] * x[j];
+    ss = __shfl(sm::tree_sum64(ss), 0, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+    float *yr = Y + (int64_t)row * cols;
+    _Float16 *hr = hl + (int64_t)row * NJ * 128 + k_position(lane);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        float y = x[j] * inv * w[j];
+        yr[lane + 64 * j] = y;
+        // The split starts from the stored f32 value: without this the
+        // compiler rounds the product to fp16 directly (v_fma_mixlo_f16),
+        // which differs from rounding the f32 result at ties.
+        asm volatile("" : "+v"(y));
+        const _Float16 h = (_Float16)y;
+        hr[128 * j] = h;
+        hr[128 * j + 64] = (_Float16)(y - (float)h);
+    }
+}
+
 // SiLU for the fused prefill epilogue, whose outputs are checked to a
 // tolerance (1e-4 + 1e-3 |e|): exp through the hardware v_exp_f32 (2^x) and a
 // hardware reciprocal, a few ulp from the libm form.
@@ -131,9 +170,7 @@ __device__ __forceinline__ PairMagic pair_magic() {
     return m;
 }
 __device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t mask, uint32_t bits) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "s"(bits));
-    return r;
+    return (a & mask) | bits;  // v_and_or_b32: mask in a VGPR, bits in an SGPR
 }
 template <int Q>
 __device__ __forceinline__ half2v pair_q(uint32_t wq, const PairMagic &m, half2v scale) {
@@ -963,6 +1000,12 @@ constexpr int kSmallBatch = 64;
 constexpr int kSmallBatchColumnTiles = 2;  // column tiles per wave of the 16-row kernel up to kSmallBatch tokens
 // Largest batch whose shared-expert products run beside the router.
 constexpr int kSharedFirstMaxTokens = 1024;
+// Largest batch that runs on one stream (no second-stream work at all). A
+// fork and join of the second stream inside a graph cost more than the
+// overlap gains below it: A/B on one GPU, graph replays of 8 stack blocks,
+// 32 tokens 87.8 -> 72.1 us, 64 tokens 108 -> 94, 128 tokens 166 -> 150,
+// 256 tokens 198 -> 186; the T=512 layer unchanged (0.269-0.274 ms).
+constexpr int kOneStreamMaxTokens = 512;
 inline int tiling_split(int tokens) { return tokens <= kSmallBatch ? kSmallBatch + 1 : 33; }
 
 // Grid bounds of the two tilings over the experts + 1 segments of m rows:
@@ -1028,15 +1071,6 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     PrefillWs w = prefill_ws(tokens, width, ff, experts, topk, block != nullptr);
     char *ws = (char *)workspace;
     const float *resid = nullptr;
-    if (block) {
-        // The stage runs on RMSNorm(X) and the combine adds X back.
-        if (int rc = norm_launch(ctx, (const float *)X, (const float *)block->gamma, (float *)(ws + w.Xn), width,
-                                 tokens, block->eps))
-            return rc;
-        resid = (const float *)X;
-        X = (uint64_t)(ws + w.Xn);
-    }
-    BlobLayout L = blob_layout(width, ff);
     if ((2 * ff) % 128 || width % 128)
         return fail(ctx, SM_E_ARG, "prefill needs width and 2*ff to be multiples of 128");
     // Streaming kernels: N a multiple of 256 and K one of the compiled group
@@ -1045,6 +1079,28 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     // tiles, else in one 32-row tile; longer ones in 64-row tiles.
     auto streamable = [](int k) { return k == 512 || k == 640 || k == 2048 || k == 2560; };
     const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && streamable(width) && streamable(ff);
+    // Batches of up to kOneStreamMaxTokens tokens (streaming shapes) run on
+    // one stream: the split before the router (in the stack block, written
+    // by the normalisation from the same registers) and the shared expert's
+    // segment tiled with the routed ones.
+    const bool one_stream = stream && tokens <= kOneStreamMaxTokens;
+    const bool hilo_in_norm = one_stream && block && (width == 2048 || width == 2560);
+    if (block) {
+        // The stage runs on RMSNorm(X) and the combine adds X back.
+        if (hilo_in_norm) {
+            const unsigned nb = (unsigned)((tokens + 3) / 4);
+            auto kn = width == 2048 ? k_norm_hilo<32> : k_norm_hilo<40>;
+            kn<<<nb, 256, 0, ctx->stream>>>((const float *)X, (const float *)block->gamma, (float *)(ws + w.Xn),
+                                            (_Float16 *)(ws + w.Xhl), tokens, block->eps);
+            if (int rc = launched(ctx)) return rc;
+        } else if (int rc = norm_launch(ctx, (const float *)X, (const float *)block->gamma, (float *)(ws + w.Xn),
+                                        width, tokens, block->eps)) {
+            return rc;
+        }
+        resid = (const float *)X;
+        X = (uint64_t)(ws + w.Xn);
+    }
+    BlobLayout L = blob_layout(width, ff);
     const int split = stream ? tiling_split(tokens) : 33;
     const int64_t routed_rows = (int64_t)tokens * topk;  // the shared expert's segment starts here
     const _Float16 *xhl = (const _Float16 *)(ws + w.Xhl), *hhl = (const _Float16 *)(ws + w.Hhl);
@@ -1084,20 +1140,24 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     // weight rows per block of the 16-row kernel for K
     auto small_bn = [small_nt](int K) { return K == 640 ? 256 : 64 * small_nt; };
 
-    // Second stream, from the start: X's hi/lo split, then (streaming shapes,
-    // up to kSharedFirstMaxTokens tokens) the shared expert's gate/up and down
-    // products over every token, which need no routing; they run beside the
-    // router and the dispatch. At larger T the router's VALU work fills the
-    // GPU and the shared products only slow it down (T=2048: layer 2 % slower
-    // in an A/B on one GPU; T=512: 1-2.5 % faster), so the dispatch tiles the
-    // shared segment with the routed ones there.
-    const bool shared_first = stream && tokens <= kSharedFirstMaxTokens;
-    if (int rc = fork_aux(ctx)) return rc;
-    const int64_t groups = (int64_t)tokens * (width / 64);
-    k_split_hilo<<<(unsigned)((groups * 8 + 255) / 256), 256, 0, ctx->aux>>>((const float *)X,
-                                                                            (_Float16 *)(ws + w.Xhl), groups);
-    int rc = launched(ctx);
-    if (rc == SM_OK) rc = aux_mark(ctx);  // the hi/lo activations are ready here
+    // Second stream (batches beyond kOneStreamMaxTokens, or shapes without
+    // the streaming kernels), from the start: X's hi/lo split, then (streaming
+    // shapes, up to kSharedFirstMaxTokens tokens) the shared expert's gate/up
+    // and down products over every token, which need no routing; they run
+    // beside the router and the dispatch. At larger T the router's VALU work
+    // fills the GPU and the shared products only slow it down (T=2048: layer
+    // 2 % slower in an A/B on one GPU), so the dispatch tiles the shared
+    // segment with the routed ones there, as it does on one stream.
+    const bool shared_first = stream && !one_stream && tokens <= kSharedFirstMaxTokens;
+    const bool aux = !one_stream;  // the second stream holds work from here to the combine
+    int rc = aux ? fork_aux(ctx) : SM_OK;
+    if (rc == SM_OK && !hilo_in_norm) {
+        const int64_t groups = (int64_t)tokens * (width / 64);
+        k_split_hilo<<<(unsigned)((groups * 8 + 255) / 256), 256, 0, aux ? ctx->aux : ctx->stream>>>(
+            (const float *)X, (_Float16 *)(ws + w.Xhl), groups);
+        rc = launched(ctx);
+    }
+    if (rc == SM_OK && aux) rc = aux_mark(ctx);  // the hi/lo activations are ready here
     if (rc == SM_OK && shared_first) {
         // The shared segment in 64-row tiles when it is long enough for them
         // (the routed segments' rule), else in 16-row tiles.
@@ -1123,23 +1183,24 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         }
     }
     if (rc) {
-        (void)join_aux(ctx);
+        if (aux) (void)join_aux(ctx);
         return rc;
     }
 
-    // From here on the second stream holds work: every early return joins
+    // From here on the second stream may hold work: every early return joins
     // it first, so a capture stays valid and no aux kernel outlives the call.
-    auto bail = [ctx](int code) {
-        (void)join_aux(ctx);
+    auto bail = [ctx, aux](int code) {
+        if (aux) (void)join_aux(ctx);
         return code;
     };
+    auto wait_split = [ctx, aux]() { return aux ? wait_aux_mark(ctx) : SM_OK; };
     if (int rc2 = stage_mark(ctx, kStagePrefillRoute)) return bail(rc2);
     if (route_cert_applies(tokens, width, experts, topk)) {
         // The certified router: W_r's fp16 copy here while the second stream
         // splits X, then the approximate logits from both.
         if (int rc2 = route_cert_prepare(ctx, (const float *)Wr, tokens, width, experts, ws + w.rcert))
             return bail(rc2);
-        if (int rc2 = wait_aux_mark(ctx)) return bail(rc2);
+        if (int rc2 = wait_split()) return bail(rc2);
         if (int rc2 = route_cert_launch(ctx, (const float *)X, xhl, tokens, width, (const float *)Wr,
                                         (const float *)bias, experts, topk, (int *)ids, (float *)weights,
                                         (const float *)Wsg, (float *)(ws + w.gate), ws + w.rcert))
@@ -1162,7 +1223,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
                                   (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch,
                                   shared_first ? 0 : 1, &tiling))
         return bail(rc2);
-    if (int rc2 = wait_aux_mark(ctx)) return bail(rc2);
+    if (int rc2 = wait_split()) return bail(rc2);
     const uint64_t m = (uint64_t)tokens * topk + tokens;
     const uint64_t segs = (uint64_t)experts + 1;
     // Segment tilings: `split` or more rows in 64-row tiles ("big"), fewer in
@@ -1222,7 +1283,8 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     if (int rc2 = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return bail(rc2);
     // Everything on the second stream (the shared expert's products) is in
     // before the combine reads P.
-    if (int rc2 = join_aux(ctx)) return rc2;
+    if (aux)
+        if (int rc2 = join_aux(ctx)) return rc2;
     if (int rc2 = stage_mark(ctx, kStagePrefillCombine)) return rc2;
     // One thread per four output columns: every load of a thread is issued
     // at once (a 2048-wide row is two blocks).

@@ -54,3 +54,24 @@ def test_real_geometry_layer(backend, oracle, real_layer, tokens, bias):
                                    host["Wsg"], W, F, E, K, bias=b)
     assert np.array_equal(eids, got_ids)
     assert tol_ok(got_y, eY), "max abs err %g" % np.abs(got_y - eY).max()
+
+
+@pytest.mark.parametrize("tokens", [1, 40, 512])
+def test_real_geometry_block_matches_separate_steps(backend, real_layer, tokens):
+    # sm_moe_block at hidden 2560 (normalisation folded into the single
+    # launch at one token, into the normalisation that also writes the GEMMs'
+    # hi/lo activations up to 512 tokens) against strata_norm, sm_moe_layer
+    # and strata_elementwise one after the other: the same bits.
+    stacks = [wl.DeviceStack(backend, layers=[real_layer], tokens=tokens, width=W, ff=F, experts=E, topk=K,
+                             trace=True, fused=f) for f in (True, False)]
+    try:
+        for st in stacks:
+            st.input(wl.BASE_SEED + 91 + tokens)
+            st.step()
+        a, b = (backend.read(st.H[1]) for st in stacks)
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.array_equal(backend.read(stacks[0].ids[0]), backend.read(stacks[1].ids[0]))
+    finally:
+        for st in stacks:
+            st.free()
