@@ -181,7 +181,7 @@ int sm_moe_dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts
  * ff/4 B), gate/up fp16 scales, down fp16 scales; 64-weight groups; weight =
  * (code - 1) * scale. width and ff must be multiples of 64.
  * ids/weights (tokens x topk) receive the routing. workspace must hold
- * sm_moe_layer_workspace(...) bytes. Up to 16 tokens run the decode kernels
+ * sm_moe_layer_workspace(...) bytes. Up to 6 tokens run the decode kernels
  * (GEMV, one grid slice per token); more tokens run dispatch + grouped MFMA
  * GEMMs. */
 int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes);
@@ -208,10 +208,12 @@ int sm_moe_route_stats(sm_ctx *ctx, uint64_t workspace, int tokens, int width, i
 /* Allocation-free variant of sm_moe_layer for the decode path (no reference
  * counterpart: it is for callers that cannot allocate, such as code under
  * HIP graph capture or a serving loop that forbids hipMalloc). Same
- * arguments and results as sm_moe_layer without the workspace: the decode
- * scratch (router logits, per-group fixed-point activations, hidden rows)
- * lives in a static device array of 2 MiB per GPU, held until the process
- * ends. Runs the decode kernels only: tokens <= 16, and the shape's decode
+ * arguments as sm_moe_layer without the workspace: the decode scratch
+ * (router logits, per-group fixed-point activations, hidden rows) lives in a
+ * static device array of 2 MiB per GPU, held until the process ends. Runs
+ * the decode kernels only: up to 6 tokens the same bits as sm_moe_layer
+ * (which runs them too), from 7 to 16 the same routing and outputs within
+ * the layer tolerance of its GEMM path. tokens <= 16, and the shape's decode
  * scratch must fit in 2 MiB (hidden 2048 / ff 512 / 512 experts / top-10
  * needs 512 KiB at 16 tokens); larger requests fail with SM_E_ARG. Nothing
  * is allocated (no hipMalloc / hipFree) and the scratch needs no clearing:
@@ -228,9 +230,10 @@ int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64
  * sm_moe_layer, and strata_elementwise mode 5, :230-236):
  *   Hout = H + MoE(RMSNorm(H; gamma, eps))          per token.
  * gamma is [width] f32. Results are bit-identical to running those three
- * steps separately. Up to 16 tokens fold the normalisation into the router
+ * steps separately. Up to 6 tokens fold the normalisation into the router
  * kernel and the residual into the down kernel; more tokens normalise into
- * the workspace and add the residual in the combine. Hout may be H itself;
+ * the workspace (up to 512 tokens together with the GEMMs' fp16 hi/lo
+ * activations) and add the residual in the combine. Hout may be H itself;
  * otherwise it must not overlap H. workspace must hold
  * sm_moe_block_workspace(...) bytes. */
 int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes);

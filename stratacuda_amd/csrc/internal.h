@@ -171,11 +171,15 @@ struct BlockArgs {
     uint64_t gamma;
     float eps;
 };
-// Batches of up to kDecodeMaxTokens tokens run the decode (GEMV) kernels with
-// a token dimension; larger ones the dispatch + grouped GEMM path (faster from
-// about 17 tokens on: 20 tokens 96 against 107 us per layer, 24 tokens 103
-// against 124 us).
+// The decode (GEMV) kernels take a token dimension of up to kDecodeMaxTokens
+// tokens (the allocation-free entry runs them up to there). sm_moe_layer and
+// sm_moe_block run them up to kDecodeBatchMaxTokens tokens and the dispatch +
+// grouped GEMM path beyond it: graph replays of 8 stack blocks on one GPU,
+// decode kernels vs GEMM path, 2 tokens 22.5 vs 35.2 us per block, 4 tokens
+// 33.1 vs 40.8, 6 tokens 45.2 vs 45.3, 8 tokens 53.8 vs 46.6, 12 tokens 71.7
+// vs 55.5, 16 tokens 89.8 vs 57.3.
 constexpr int kDecodeMaxTokens = 16;
+constexpr int kDecodeBatchMaxTokens = 6;
 constexpr int kDecodeBlockRouting = 4;  // up to this many tokens the gate/up blocks route
 constexpr int kRouteRowsMaxTokens = 8;  // router logits one wave per (row, token) up to here
 // Exact per-token top-k (strata_router order) of logits [tokens x experts].

@@ -508,7 +508,7 @@ int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps,
         if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
     if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
     if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
-    uint64_t ws = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
+    uint64_t ws = tokens <= kDecodeBatchMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                               : moe_prefill_workspace(tokens, width, ff, experts, topk, true);
     if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
     if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
@@ -516,7 +516,7 @@ int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps,
         return fail(ctx, SM_E_ARG, "Hout must be H itself or not overlap it");
     const BlockArgs block = {gamma, eps};
     check_prefetch(ctx);
-    if (tokens <= kDecodeMaxTokens)
+    if (tokens <= kDecodeBatchMaxTokens)
         return clear_prefetch(ctx, moe_decode(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
                                               experts, topk, Hout, ids, weights, workspace, workspace_bytes, &block));
     return clear_prefetch(ctx, moe_prefill(ctx, H, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
@@ -525,7 +525,7 @@ int sm_moe_block(sm_ctx *ctx, uint64_t H, int tokens, uint64_t gamma, float eps,
 
 int sm_moe_block_workspace(int tokens, int width, int ff, int experts, int topk, uint64_t *bytes) {
     if (int rc = sm_moe_layer_workspace(tokens, width, ff, experts, topk, bytes)) return rc;
-    if (tokens > kDecodeMaxTokens) *bytes = moe_prefill_workspace(tokens, width, ff, experts, topk, true);
+    if (tokens > kDecodeBatchMaxTokens) *bytes = moe_prefill_workspace(tokens, width, ff, experts, topk, true);
     return SM_OK;
 }
 
@@ -533,7 +533,7 @@ int sm_moe_layer_workspace(int tokens, int width, int ff, int experts, int topk,
     if (!bytes || tokens < 1 || width < 64 || ff < 64 || width % 64 || ff % 64 || experts < 1 || experts > 512 ||
         topk < 1 || topk > 32 || topk > experts)
         return SM_E_ARG;
-    *bytes = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
+    *bytes = tokens <= kDecodeBatchMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                          : moe_prefill_workspace(tokens, width, ff, experts, topk);
     return SM_OK;
 }
@@ -544,7 +544,7 @@ int sm_moe_route_stats(sm_ctx *ctx, uint64_t workspace, int tokens, int width, i
     if (ctx->capturing) return fail(ctx, SM_E_ARG, "not allowed while capturing a graph");
     *candidates = 0;
     *fallbacks = 0;
-    if (tokens <= kDecodeMaxTokens) return 0;
+    if (tokens <= kDecodeBatchMaxTokens) return 0;
     const int64_t off = moe_prefill_route_stats_offset(tokens, width, ff, experts, topk);
     if (off < 0) return 0;
     if (int rc = need(ctx, workspace, (uint64_t)off + (uint64_t)tokens * 4, "workspace")) return rc;
@@ -610,12 +610,12 @@ int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias
         if (int rc = need(ctx, bias, (uint64_t)experts * 4, "router bias")) return rc;
     if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
     if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
-    uint64_t ws = tokens <= kDecodeMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
+    uint64_t ws = tokens <= kDecodeBatchMaxTokens ? moe_decode_workspace(tokens, width, ff, experts, topk)
                               : moe_prefill_workspace(tokens, width, ff, experts, topk);
     if (workspace_bytes < ws) return fail(ctx, SM_E_ARG, "workspace too small");
     if (int rc = need(ctx, workspace, ws, "workspace")) return rc;
     check_prefetch(ctx);
-    if (tokens <= kDecodeMaxTokens)
+    if (tokens <= kDecodeBatchMaxTokens)
         return clear_prefetch(ctx, moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
                                               experts, topk, Y, ids, weights, workspace, workspace_bytes));
     return clear_prefetch(ctx, moe_prefill(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,

@@ -23,7 +23,7 @@ def bits(a):
     return np.asarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("tokens", [1, 8, 20, 40, 512])
+@pytest.mark.parametrize("tokens", [1, 4, 8, 20, 40, 512])
 @pytest.mark.parametrize("block", [False, True])
 def test_graph_replay_matches_eager(backend, layers, tokens, block):
     b = backend

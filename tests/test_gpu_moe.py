@@ -219,10 +219,10 @@ def routing_styles(E):
     return styles
 
 
-@pytest.mark.parametrize("tokens", [1, 3, 8, 20, 30, CERTIFIED_MIN_TOKENS])
+@pytest.mark.parametrize("tokens", [1, 3, 6, 8, 20, 30, CERTIFIED_MIN_TOKENS])
 def test_layer_routing_edge_logits(backend, oracle, full_layer, tokens):
     # W_r = 0 makes every logit exactly the per-expert bias, so the layer's
-    # routing (the in-block top-k up to 4 tokens, the top-k kernel up to 16,
+    # routing (the in-block top-k up to 4 tokens, the top-k kernel up to 6,
     # the exact prefill router up to 511, the certified router from 512 on)
     # sees ties, underflow to 0, NaN and +-inf. (With W_r = 0 the certified
     # router's approximate logits are exact, so its weights are too.)
@@ -239,11 +239,11 @@ def test_layer_routing_edge_logits(backend, oracle, full_layer, tokens):
         assert same_bits(backend.read(w), rw), name
 
 
-@pytest.mark.parametrize("tokens", [16, 17, 24, 25, 40, 64, 65])
+@pytest.mark.parametrize("tokens", [5, 6, 7, 16, 17, 24, 25, 40, 64, 65])
 def test_layer_small_batch_full(backend, oracle, full_layer, tokens):
-    # 16 tokens: the decode kernels with a token dimension (one top-k kernel
-    # for the batch); 17..64: 16-row tiles over every segment; 65: the first
-    # batch with 64-row tiles.
+    # 5 and 6 tokens: the decode kernels with a token dimension (one top-k
+    # kernel for the batch); 7..64: 16-row tiles over every segment on one
+    # stream; 65: the first batch with 64-row tiles.
     check_full_layer(backend, oracle, full_layer, tokens, False)
 
 

@@ -30,8 +30,8 @@ def test_real_blob_layout(real_layer):
     assert real_layer.stride >= 1382400 and real_layer.stride % 256 == 0
 
 
-@pytest.mark.parametrize("tokens,bias", [(1, False), (1, True), (8, False), (24, False), (40, False), (512, False),
-                                         (2048, True)])
+@pytest.mark.parametrize("tokens,bias", [(1, False), (1, True), (6, False), (8, False), (24, False), (40, False),
+                                         (512, False), (2048, True)])
 def test_real_geometry_layer(backend, oracle, real_layer, tokens, bias):
     layer = real_layer
     X = backend.alloc(tokens * W, "f32", zero=False)

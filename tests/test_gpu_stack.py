@@ -142,7 +142,7 @@ def test_stack_batch32(backend, oracle, stack_layers):
         st.free()
 
 
-@pytest.mark.parametrize("tokens", [1, 8, 32, 100, 512])
+@pytest.mark.parametrize("tokens", [1, 4, 8, 32, 100, 512])
 def test_block_entry_matches_separate_steps(backend, stack_layers, tokens):
     """sm_moe_block (normalisation and residual folded into the stage) gives
     the same bits as strata_norm, sm_moe_layer and strata_elementwise run

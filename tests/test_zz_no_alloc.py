@@ -1,12 +1,18 @@
-"""The allocation-free decode entry (sm_moe_layer_static) through the C ABI:
-its results are the bits of sm_moe_layer with a workspace, on two calls in a
-row, the second with fewer tokens; it allocates nothing, and it refuses
-shapes beyond its static scratch with a clear error."""
+"""The allocation-free decode entry (sm_moe_layer_static) through the C ABI
+against sm_moe_layer with a workspace, on two calls in a row, the second with
+fewer tokens: up to 6 tokens both run the decode kernels and give the same
+bits; from 7 to 16 tokens sm_moe_layer runs the grouped GEMMs, so the routing
+(IDs and weights) is the same bits and the outputs agree within
+1e-4 + 1e-3 |e|. It allocates nothing, and it refuses shapes beyond its
+static scratch with a clear error."""
 import numpy as np
 import pytest
 
 import stratacuda_amd as sm
+from conftest import tol_ok
 from stratacuda_amd import workload as wl
+
+DECODE_BATCH_MAX = 6  # sm_moe_layer runs the decode kernels up to here
 
 pytestmark = pytest.mark.gpu
 
@@ -29,7 +35,8 @@ def _layer(backend, layers, width, ff):
     return layers[(width, ff)]
 
 
-@pytest.mark.parametrize("width,ff,token_seq", [(2048, 512, (8, 1)), (2048, 512, (16, 3)), (2560, 640, (5, 1))])
+@pytest.mark.parametrize("width,ff,token_seq", [(2048, 512, (8, 1)), (2048, 512, (16, 3)), (2048, 512, (6, 2)),
+                                                (2560, 640, (5, 1))])
 def test_static_entry_matches_workspace_entry(backend, layers, width, ff, token_seq):
     b = backend
     E, K = wl.EXPERTS, wl.TOPK
@@ -55,7 +62,10 @@ def test_static_entry_matches_workspace_entry(backend, layers, width, ff, token_
         assert np.array_equal(bits(b.read(w, count=nk)), bits(b.read(w_ref, count=nk))), (call, T)
         got, want = b.read(Y, count=n), b.read(Y_ref, count=n)
         assert np.all(np.isfinite(got))
-        assert np.array_equal(bits(got), bits(want)), (call, T, float(np.abs(got - want).max()))
+        if T <= DECODE_BATCH_MAX:
+            assert np.array_equal(bits(got), bits(want)), (call, T, float(np.abs(got - want).max()))
+        else:
+            assert tol_ok(got, want), (call, T, float(np.abs(got - want).max()))
     for buf in (X, Y_ref, Y, ids_ref, ids, w_ref, w, ws):
         b.free(buf)
 
