@@ -33,9 +33,8 @@
 //    v_mfma_f32_16x16x32_f16 (k_moe_gemm_rows16, k_moe_gemm_stream16); the
 //    two grids cover disjoint rows and run on two streams. Each block reads
 //    its tile record (segment, first row, end row, segment start) written by
-//    the dispatch, or for the shared expert's segment by k_shared_tiles: the
-//    shared expert needs no routing, so its GEMMs run on the second stream
-//    from the start, beside the router and the dispatch.
+//    the dispatch, which tiles the shared expert's segment (every token) with
+//    the routed ones.
 //    Other shapes use k_moe_gemm (register-held B, A double-buffered in LDS,
 //    64- and 32-row tiles).
 //    grid.x = n-block (fastest) so the m-tiles of one (expert, n-block) run
@@ -923,17 +922,6 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
         }
 }
 
-// Tile records of the shared expert's segment, rows [first, first + rows)
-// (every token in order), in tiles of mt rows: tiles[experts + 1] = count and
-// record j = (experts, first + j mt, first + rows, first), the layout the
-// dispatch writes for the routed segments.
-__global__ void k_shared_tiles(int4 *__restrict__ info, int *__restrict__ tiles, int experts, int first, int rows,
-                               int mt) {
-    const int n = (rows + mt - 1) / mt;
-    for (int j = threadIdx.x; j < n; j += blockDim.x) info[j] = make_int4(experts, first + j * mt, first + rows, first);
-    if (threadIdx.x == 0) tiles[experts + 1] = n;
-}
-
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
 // in the reference order (kernels/strata.cu:470-476); with `resid`,
 // Y = resid + that (strata_elementwise mode 5). One block per token:
@@ -998,14 +986,6 @@ inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // tile segments of more than 32 rows in 64-row tiles.
 constexpr int kSmallBatch = 64;
 constexpr int kSmallBatchColumnTiles = 2;  // column tiles per wave of the 16-row kernel up to kSmallBatch tokens
-// Largest batch whose shared-expert products run beside the router.
-constexpr int kSharedFirstMaxTokens = 1024;
-// Largest batch that runs on one stream (no second-stream work at all). A
-// fork and join of the second stream inside a graph cost more than the
-// overlap gains below it: A/B on one GPU, graph replays of 8 stack blocks,
-// 32 tokens 87.8 -> 72.1 us, 64 tokens 108 -> 94, 128 tokens 166 -> 150,
-// 256 tokens 198 -> 186; the T=512 layer unchanged (0.269-0.274 ms).
-constexpr int kOneStreamMaxTokens = 512;
 inline int tiling_split(int tokens) { return tokens <= kSmallBatch ? kSmallBatch + 1 : 33; }
 
 // Grid bounds of the two tilings over the experts + 1 segments of m rows:
@@ -1022,7 +1002,7 @@ inline uint64_t big_tile_bound(uint64_t m, int experts) {
 }
 
 struct PrefillWs {
-    uint64_t logits, rcert, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big, tiles_shared, info_shared,
+    uint64_t logits, rcert, gate, dispatch, offsets, tiles_small, tiles_big, info_small, info_big,
         rows, parts, where_, Xhl, Hhl, P, Xn, end;
 };
 PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool block = false) {
@@ -1037,9 +1017,7 @@ PrefillWs prefill_ws(int tokens, int width, int ff, int experts, int topk, bool 
     w.tiles_big = up(w.tiles_small + ((uint64_t)experts + 2) * 4);
     w.info_small = up(w.tiles_big + ((uint64_t)experts + 2) * 4);
     w.info_big = up(w.info_small + small_tile_bound(m, experts, tiling_split(tokens)) * 16);
-    w.tiles_shared = up(w.info_big + big_tile_bound(m, experts) * 16);
-    w.info_shared = up(w.tiles_shared + ((uint64_t)experts + 2) * 4);
-    w.rows = up(w.info_shared + ((uint64_t)tokens / 16 + 1) * 16);
+    w.rows = up(w.info_big + big_tile_bound(m, experts) * 16);
     w.parts = up(w.rows + m * 4);
     w.where_ = up(w.parts + m * 4);
     w.Xhl = up(w.where_ + n * 4);
@@ -1079,11 +1057,16 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     // tiles, else in one 32-row tile; longer ones in 64-row tiles.
     auto streamable = [](int k) { return k == 512 || k == 640 || k == 2048 || k == 2560; };
     const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && streamable(width) && streamable(ff);
-    // Batches of up to kOneStreamMaxTokens tokens (streaming shapes) run on
-    // one stream: the split before the router (in the stack block, written
-    // by the normalisation from the same registers) and the shared expert's
-    // segment tiled with the routed ones.
-    const bool one_stream = stream && tokens <= kOneStreamMaxTokens;
+    // Streaming shapes issue the split, the router and the dispatch on the
+    // library's stream: a fork to the second stream and the join back inside
+    // a graph cost more than the overlap they buy (A/B on one GPU, graph
+    // replays: 8 stack blocks of 32 tokens 87.8 -> 72.1 us, 64 tokens 108 ->
+    // 94, 128 tokens 166 -> 150, 256 tokens 198 -> 186; the T=2048 layer
+    // 0.462 -> 0.455 ms, T=512 unchanged; the shared expert's products had
+    // run on the second stream beside the router, now the dispatch tiles its
+    // segment with the routed ones). In the stack block the normalisation
+    // writes the split itself, from the same registers.
+    const bool one_stream = stream;
     const bool hilo_in_norm = one_stream && block && (width == 2048 || width == 2560);
     if (block) {
         // The stage runs on RMSNorm(X) and the combine adds X back.
@@ -1140,15 +1123,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     // weight rows per block of the 16-row kernel for K
     auto small_bn = [small_nt](int K) { return K == 640 ? 256 : 64 * small_nt; };
 
-    // Second stream (batches beyond kOneStreamMaxTokens, or shapes without
-    // the streaming kernels), from the start: X's hi/lo split, then (streaming
-    // shapes, up to kSharedFirstMaxTokens tokens) the shared expert's gate/up
-    // and down products over every token, which need no routing; they run
-    // beside the router and the dispatch. At larger T the router's VALU work
-    // fills the GPU and the shared products only slow it down (T=2048: layer
-    // 2 % slower in an A/B on one GPU), so the dispatch tiles the shared
-    // segment with the routed ones there, as it does on one stream.
-    const bool shared_first = stream && !one_stream && tokens <= kSharedFirstMaxTokens;
+    // Other shapes: the split on the second stream, beside the router.
     const bool aux = !one_stream;  // the second stream holds work from here to the combine
     int rc = aux ? fork_aux(ctx) : SM_OK;
     if (rc == SM_OK && !hilo_in_norm) {
@@ -1158,30 +1133,6 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         rc = launched(ctx);
     }
     if (rc == SM_OK && aux) rc = aux_mark(ctx);  // the hi/lo activations are ready here
-    if (rc == SM_OK && shared_first) {
-        // The shared segment in 64-row tiles when it is long enough for them
-        // (the routed segments' rule), else in 16-row tiles.
-        const bool big = tokens >= split;
-        const int mt = big ? 64 : 16, ntiles = ((tokens + mt - 1) / mt + 7) / 8 * 8;  // grid: multiple of 8
-        int4 *info_sh = (int4 *)(ws + w.info_shared);
-        int *tiles_sh = (int *)(ws + w.tiles_shared);
-        k_shared_tiles<<<1, 256, 0, ctx->aux>>>(info_sh, tiles_sh, experts, (int)routed_rows, tokens, mt);
-        rc = launched(ctx);
-        if (rc == SM_OK) {
-            const KT k = big ? big_kernel(true, width) : small_kernel(true, width);
-            k<<<dim3((unsigned)(2 * ff / (big ? 256 : small_bn(width))), (unsigned)ntiles), 256, 0, ctx->aux>>>(
-                xhl, (const int *)(ws + w.rows), info_sh, tiles_sh, ar, blob_stride, sh, experts, L.gate_up_codes, L.gate_up_scales,
-                width, 2 * ff, ws + w.Hhl, ff);
-            rc = launched(ctx);
-        }
-        if (rc == SM_OK) {
-            const KT k = big ? big_kernel(false, ff) : small_kernel(false, ff);
-            k<<<dim3((unsigned)(width / (big ? 256 : small_bn(ff))), (unsigned)ntiles), 256, 0, ctx->aux>>>(
-                hhl, nullptr, info_sh, tiles_sh, ar, blob_stride, sh, experts, L.down_codes, L.down_scales, ff, width,
-                ws + w.P, width);
-            rc = launched(ctx);
-        }
-    }
     if (rc) {
         if (aux) (void)join_aux(ctx);
         return rc;
@@ -1217,11 +1168,9 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     GemmTiling tiling = {tiles_small, tiles_big, split, stream ? 16 : 32, 64};
     tiling.info_small = (int *)info_small;
     tiling.info_big = (int *)info_big;
-    // The dispatch tiles the shared expert's segment only where it is not
-    // computed on the second stream already.
+    // The dispatch also tiles the shared expert's segment (every token).
     if (int rc2 = dispatch_launch(ctx, (const int *)ids, tokens, topk, experts, offsets, (int *)(ws + w.rows),
-                                  (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch,
-                                  shared_first ? 0 : 1, &tiling))
+                                  (int *)(ws + w.parts), (int *)(ws + w.where_), ws + w.dispatch, 1, &tiling))
         return bail(rc2);
     if (int rc2 = wait_split()) return bail(rc2);
     const uint64_t m = (uint64_t)tokens * topk + tokens;
