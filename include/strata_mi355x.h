@@ -217,9 +217,12 @@ int sm_moe_route_stats(sm_ctx *ctx, uint64_t workspace, int tokens, int width, i
  * scratch must fit in 2 MiB (hidden 2048 / ff 512 / 512 experts / top-10
  * needs 512 KiB at 16 tokens); larger requests fail with SM_E_ARG. Nothing
  * is allocated (no hipMalloc / hipFree) and the scratch needs no clearing:
- * every word a call reads, that call wrote first. Calls that overlap on one
- * GPU (two streams or two contexts at once) share the array and race; calls
- * in stream order do not. Refused while stage timing is enabled. */
+ * every word a call reads, that call wrote first. Every call on one GPU
+ * shares the array; a call on another stream (or context) than the previous
+ * one waits for that call on the GPU, so such calls run in turn instead of
+ * racing. Calls on a capturing stream are not ordered by the library (the
+ * caller orders them within its graph). Refused while stage timing is
+ * enabled. */
 int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,
                         uint64_t blob_stride, uint64_t shared_blob, uint64_t Wsg, int width, int ff,
                         int experts, int topk, uint64_t Y, uint64_t ids, uint64_t weights);

@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -195,6 +196,23 @@ uint64_t moe_decode_workspace(int tokens, int width, int ff, int experts, int to
 constexpr uint64_t kStaticScratchBytes = 2ull << 20;
 constexpr int kMaxDevices = 64;
 int static_scratch_init(sm_ctx *ctx);
+// One allocation-free call's use of the device's static scratch: holds the
+// device's lock while the call is enqueued; begin() makes the call's stream
+// wait for the previous such call when that ran on another stream, so calls
+// from two streams or contexts run one after the other instead of racing on
+// the shared array; done() records the call's end. Calls on a capturing
+// stream are neither ordered nor recorded.
+class StaticScratchCall {
+  public:
+    explicit StaticScratchCall(sm_ctx *ctx);
+    int begin();
+    int done();
+
+  private:
+    sm_ctx *ctx_;
+    std::lock_guard<std::mutex> lock_;
+    bool capturing_ = false;
+};
 // Size of ctx->attn_scores: 1,024 (token, head) rows of 2,048 cells.
 constexpr uint64_t kAttnScoresBytes = 1024ull * 2048 * 4;
 int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena,

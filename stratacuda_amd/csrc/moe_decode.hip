@@ -1526,20 +1526,67 @@ static __device__ __align__(256) uint8_t scratch[smi::kStaticScratchBytes];
 
 namespace smi {
 
+namespace {
+// Per device: the scratch address, and the end of the last allocation-free
+// call (its stream and an event recorded there), under one lock.
+struct StaticScratchState {
+    std::mutex lock;
+    void *ptr = nullptr;
+    hipEvent_t last = nullptr;
+    hipStream_t last_stream = nullptr;
+    bool pending = false;  // `last` marks the end of a call not yet waited for by its successor
+};
+StaticScratchState g_static[kMaxDevices];
+}  // namespace
+
 int static_scratch_init(sm_ctx *ctx) {
     // One lookup per device; every context on that device shares the array.
-    static std::mutex lock;
-    static void *by_device[kMaxDevices] = {};
     if (ctx->device < 0 || ctx->device >= kMaxDevices) return fail(ctx, SM_E_ARG, "device index out of range");
-    std::lock_guard<std::mutex> g(lock);
-    if (!by_device[ctx->device]) {
+    StaticScratchState &st = g_static[ctx->device];
+    std::lock_guard<std::mutex> g(st.lock);
+    if (!st.ptr) {
         void *p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
         if (!p) return fail(ctx, SM_E_HIP, "hipGetSymbolAddress(scratch) returned no address");
-        by_device[ctx->device] = p;
+        hipEvent_t ev = nullptr;
+        const hipError_t e2 = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e2 != hipSuccess) return hip_fail(ctx, e2, "hipEventCreateWithFlags(static scratch)");
+        st.last = ev;
+        st.ptr = p;
     }
-    ctx->scratch = by_device[ctx->device];
+    ctx->scratch = st.ptr;
+    return SM_OK;
+}
+
+StaticScratchCall::StaticScratchCall(sm_ctx *ctx) : ctx_(ctx), lock_(g_static[ctx->device].lock) {}
+
+int StaticScratchCall::begin() {
+    StaticScratchState &st = g_static[ctx_->device];
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(ctx_->stream, &cs);
+    if (e != hipSuccess) return hip_fail(ctx_, e, "hipStreamIsCapturing");
+    capturing_ = cs != hipStreamCaptureStatusNone;
+    // Under capture the call is a graph node: its order is the caller's (an
+    // event recorded outside the capture cannot be waited for inside it).
+    if (capturing_ || !st.pending || st.last_stream == ctx_->stream) return SM_OK;
+    const hipError_t w = hipStreamWaitEvent(ctx_->stream, st.last, 0);
+    if (w != hipSuccess) return hip_fail(ctx_, w, "hipStreamWaitEvent(static scratch)");
+    return SM_OK;
+}
+
+int StaticScratchCall::done() {
+    StaticScratchState &st = g_static[ctx_->device];
+    // A captured call leaves the record as it is: the next call outside the
+    // capture still waits for the last one that ran outside it.
+    if (capturing_) return SM_OK;
+    const hipError_t e = hipEventRecord(st.last, ctx_->stream);
+    if (e != hipSuccess) {
+        st.pending = false;
+        return hip_fail(ctx_, e, "hipEventRecord(static scratch)");
+    }
+    st.last_stream = ctx_->stream;
+    st.pending = true;
     return SM_OK;
 }
 

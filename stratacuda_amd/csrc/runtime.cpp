@@ -588,8 +588,12 @@ int sm_moe_layer_static(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64
     if (int rc = need(ctx, ids, (uint64_t)tokens * topk * 4, "ids")) return rc;
     if (int rc = need(ctx, weights, (uint64_t)tokens * topk * 4, "weights")) return rc;
     check_prefetch(ctx);
-    return clear_prefetch(ctx, moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff,
-                                          experts, topk, Y, ids, weights, (uint64_t)ctx->scratch, kStaticScratchBytes));
+    StaticScratchCall use(ctx);
+    if (int rc = use.begin()) return clear_prefetch(ctx, rc);
+    const int rc = moe_decode(ctx, X, tokens, Wr, bias, arena, blob_stride, shared_blob, Wsg, width, ff, experts, topk, Y,
+                              ids, weights, (uint64_t)ctx->scratch, kStaticScratchBytes);
+    if (rc) return clear_prefetch(ctx, rc);
+    return clear_prefetch(ctx, use.done());
 }
 
 int sm_moe_layer(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias, uint64_t arena, uint64_t blob_stride,

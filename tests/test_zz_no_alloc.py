@@ -83,3 +83,52 @@ def test_static_entry_refuses_what_does_not_fit(backend, layers):
         b.moe_layer_static(X, 16, lay.Wr, lay.arena, lay.stride, lay.shared, lay.Wsg, 2048, 3072, E, K, Y, ids, w)
     for buf in (X, Y, ids, w):
         b.free(buf)
+
+
+def test_static_entry_orders_calls_from_two_contexts(backend, layers):
+    """Two contexts on one GPU (two streams) call the allocation-free entry
+    back to back without synchronising in between: each call waits for the
+    previous one on the other stream, so every result equals the same call
+    made alone."""
+    b1 = backend
+    b2 = sm.Backend(0)
+    E, K, W, F, T = wl.EXPERTS, wl.TOPK, 2048, 512, 4
+    try:
+        lay1 = _layer(b1, layers, W, F)
+        lay2 = wl.DeviceLayer(b2, layer=5)
+        X1, X2 = b1.alloc(T * W, zero=False), b2.alloc(T * W, zero=False)
+        b1.synth_normal(X1, T * W, 901, wl.STREAM_INPUT, 1.0)
+        b2.synth_normal(X2, T * W, 902, wl.STREAM_INPUT, 1.0)
+        out1 = [b1.alloc(T * W), b1.alloc(T * K, "i32"), b1.alloc(T * K)]
+        out2 = [b2.alloc(T * W), b2.alloc(T * K, "i32"), b2.alloc(T * K)]
+
+        def call1():
+            b1.moe_layer_static(X1, T, lay1.Wr, lay1.arena, lay1.stride, lay1.shared, lay1.Wsg, W, F, E, K, *out1)
+
+        def call2():
+            b2.moe_layer_static(X2, T, lay2.Wr, lay2.arena, lay2.stride, lay2.shared, lay2.Wsg, W, F, E, K, *out2)
+
+        def read(b, out):
+            return [bits(b.read(o)) if o is out[0] or o is out[2] else b.read(o) for o in out]
+
+        call1()
+        b1.sync()
+        want1 = read(b1, out1)
+        call2()
+        b2.sync()
+        want2 = read(b2, out2)
+        for rep in range(8):
+            print("static entry, two contexts: round %d" % rep, flush=True)
+            call1()
+            call2()
+            b1.sync()
+            b2.sync()
+            for got, want in zip(read(b1, out1), want1):
+                assert np.array_equal(got, want), ("context 1", rep)
+            for got, want in zip(read(b2, out2), want2):
+                assert np.array_equal(got, want), ("context 2", rep)
+        for buf in [X1] + out1:
+            b1.free(buf)
+        lay2.free()
+    finally:
+        b2.dispose()
