@@ -15,7 +15,9 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "internal.h"
 #include "strata_device.h"
@@ -221,6 +223,164 @@ __global__ void k_quant_project(const float *X, const uint32_t *Codes, const flo
     }
     sum = sm::tree_sum64(sum);
     if (lane == 0) Y[(int64_t)token * outputStride + outputOffset + row] = sum;
+}
+
+// One-token projections with whole rows staged in LDS: the same per-lane
+// sums as k_quant_project / k_bf16_project (lane l adds the products of
+// elements l, l + 64, ... in order, then the reference's tree), with the
+// loads reorganised. Each wave owns up to kRowsPerWave consecutive rows, one
+// LDS buffer each; every row's codes go out at once by 16-byte DMA (its
+// scales and offsets by 4-byte DMA), the wave waits once and sums the rows
+// from LDS, and x stays in registers (element lane + 64 j in xv[j]). The
+// generic kernels issue one narrow load per element and lane instead (64
+// lanes of a quant_gemv load touch 8 distinct words), which leaves them
+// issue-bound far below the memory's rate.
+constexpr int kRowsPerWave = 4;
+constexpr int kStagedMaxJ = 64;  // cols <= 4096: x in at most 64 registers (JB, a multiple of 8 >= cols / 64)
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void dma_lds16(const void *src, uint32_t *lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_lds4(const void *src, uint32_t *lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds_base, 4, 0, 0);
+}
+// Every DMA of this wave has landed in LDS, and no LDS access moves across.
+__device__ __forceinline__ void dma_wait_all() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
+    asm volatile("" ::: "memory");
+}
+
+// The staged row sum of k_quant_gemv_staged: lane l's products in order,
+// with the codebook and offset choices made once per row. Element
+// i = lane + 64 j: its code word is lane / EPW + 64 j / EPW (an immediate
+// offset from the lane's base), its group (64 j >> group_shift) +
+// (lane >> group_shift) for every power-of-two group size, the offset of a
+// group kStagedOffsets words after its scale.
+constexpr int kStagedOffsets = 256;  // scales at [0, 256) of a row's group area, offsets at [256, 512)
+template <int BITS, int JB, bool CODEBOOK, bool OFFSET>
+__device__ __forceinline__ float staged_quant_row(const uint32_t *codes, const float *groups, int J, int group_shift,
+                                                  int bias, const float (&xv)[JB], int lane) {
+    constexpr int EPW = 32 / BITS;
+    constexpr uint32_t MASK = (1u << BITS) - 1u;
+    const uint32_t *cl = codes + lane / EPW;
+    const int shift = (lane % EPW) * BITS;
+    const float *gl = groups + (lane >> group_shift);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < JB; j++) {
+        if (j < JB - 8 || j < J) {  // J > JB - 8
+            const int code = (int)((cl[64 / EPW * j] >> shift) & MASK);
+            const float *gj = gl + ((64 * j) >> group_shift);
+            const float value = CODEBOOK ? iq4(code) : (float)(code + bias);
+            float weight = value * gj[0];
+            if (OFFSET) weight = weight + gj[kStagedOffsets];
+            sum = sum + weight * xv[j];
+        }
+    }
+    return sum;
+}
+
+// kernels/strata.cu:134-155 strata_quant_gemv (strata_quant_project's
+// arithmetic, one token) for rows of cols % 64 == 0, cols <= 64 JB (JB - 8 <
+// cols / 64), whole 16-byte code chunks per row, a power-of-two group size
+// and at most 256 groups per row. Buffer words: codes (cw), scales (ng of
+// kStagedOffsets), offsets (ng of kStagedOffsets).
+template <int BITS, int JB>
+__global__ void __launch_bounds__(256) k_quant_gemv_staged(const float *__restrict__ X,
+                                                           const uint32_t *__restrict__ Codes,
+                                                           const float *__restrict__ Scales,
+                                                           const float *__restrict__ Offsets, float *__restrict__ Y,
+                                                           int cols, int rows, int group_shift, int bias,
+                                                           int codebook, int hasOffset, int rpw) {
+    extern __shared__ uint32_t staged[];
+    constexpr int EPW = 32 / BITS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int J = cols >> 6, cw = cols / EPW, ng = cols >> group_shift;
+    const int bufw = cw + 2 * kStagedOffsets;
+    uint32_t *bufs = staged + wave * rpw * bufw;
+    const int r0 = (blockIdx.x * 4 + wave) * rpw;
+    if (r0 >= rows) return;
+    const int nr = min(rpw, rows - r0);
+    // Every row of the wave in flight at once, then one wait.
+    for (int k = 0; k < nr; k++) {
+        const int r = r0 + k;
+        uint32_t *buf = bufs + k * bufw;
+        const uint8_t *crow = (const uint8_t *)Codes + (int64_t)r * cw * 4;
+        for (int c = 0; c < cw / 4; c += 64)
+            if (c + lane < cw / 4) dma_lds16(crow + (int64_t)(c + lane) * 16, buf + 4 * c);
+        for (int c = 0; c < ng; c += 64)
+            if (c + lane < ng) dma_lds4(Scales + (int64_t)r * ng + c + lane, buf + cw + c);
+        if (hasOffset)
+            for (int c = 0; c < ng; c += 64)
+                if (c + lane < ng) dma_lds4(Offsets + (int64_t)r * ng + c + lane, buf + cw + kStagedOffsets + c);
+    }
+    float xv[JB];
+#pragma unroll
+    for (int j = 0; j < JB; j++) xv[j] = (j < JB - 8 || j < J) ? X[lane + 64 * j] : 0.0f;
+    dma_wait_all();
+    // The codebook and offset choices select one whole row loop (with the
+    // stores inside, so the compiler cannot run the variants side by side).
+    auto rows_loop = [&](auto codebook_tag, auto offset_tag) {
+        for (int k = 0; k < nr; k++) {
+            const uint32_t *buf = bufs + k * bufw;
+            float sum = staged_quant_row<BITS, JB, decltype(codebook_tag)::value, decltype(offset_tag)::value>(
+                buf, (const float *)(buf + cw), J, group_shift, bias, xv, lane);
+            sum = sm::tree_sum64(sum);
+            if (lane == 0) Y[r0 + k] = sum;
+        }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (codebook == 1) {
+        if (hasOffset) rows_loop(T{}, T{});
+        else rows_loop(T{}, F{});
+    } else {
+        if (hasOffset) rows_loop(F{}, T{});
+        else rows_loop(F{}, F{});
+    }
+}
+
+// kernels/strata.cu:168-176 strata_bf16_project for one token and rows of
+// cols % 64 == 0, cols <= 64 JB (JB - 8 < cols / 64). Each wave sums up to
+// kRowsPerWave rows with two row buffers: the next row's DMA goes out before
+// the current row is summed.
+template <int JB>
+__global__ void __launch_bounds__(256) k_bf16_gemv_staged(const float *__restrict__ X,
+                                                          const uint32_t *__restrict__ Codes, float *__restrict__ Y,
+                                                          int cols, int rows, int outputOffset) {
+    extern __shared__ uint32_t staged[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int J = cols >> 6, cw = cols >> 1;
+    uint32_t *buf0 = staged + wave * 2 * cw, *buf1 = buf0 + cw;
+    const int r0 = (blockIdx.x * 4 + wave) * kRowsPerWave;
+    if (r0 >= rows) return;
+    auto issue = [&](int r, uint32_t *buf) {
+        const uint8_t *crow = (const uint8_t *)Codes + (int64_t)r * cw * 4;
+        for (int c = 0; c < cw / 4; c += 64)
+            if (c + lane < cw / 4) dma_lds16(crow + (int64_t)(c + lane) * 16, buf + 4 * c);
+    };
+    issue(r0, buf0);
+    float xv[JB];
+#pragma unroll
+    for (int j = 0; j < JB; j++) xv[j] = (j < JB - 8 || j < J) ? X[lane + 64 * j] : 0.0f;
+    for (int k = 0; k < kRowsPerWave; k++) {
+        const int r = r0 + k;
+        if (r >= rows) break;
+        dma_wait_all();
+        if (k + 1 < kRowsPerWave && r + 1 < rows) issue(r + 1, (k & 1) ? buf0 : buf1);
+        const uint32_t *buf = (k & 1) ? buf1 : buf0;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < JB; j++) {
+            if (j < JB - 8 || j < J) {  // J > JB - 8
+                const int i = lane + 64 * j;  // row * cols is even: element parity is i's
+                sum = sum + __uint_as_float(((buf[i >> 1] >> ((i & 1) * 16)) & 65535u) << 16) * xv[j];
+            }
+        }
+        sum = sm::tree_sum64(sum);
+        if (lane == 0) Y[outputOffset + r] = sum;
+    }
 }
 
 // kernels/strata.cu:214-227 strata_norm
@@ -549,6 +709,17 @@ int L_bf16_project(sm_ctx *ctx, const uint32_t *G, Args a) {
                                    &rr, &tt, G))
         return rc;
     if (int rc = need(ctx, a.ptr(1), ((uint64_t)rr * cols + 1) / 2 * 4, "strata_bf16_project.Codes")) return rc;
+    if (tt == 1 && cols % 64 == 0 && cols <= 64 * kStagedMaxJ && a.ptr(1) % 16 == 0) {
+        // one token: whole rows staged in LDS (same sums, same order)
+        const unsigned blocks = (unsigned)((rr + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+        using KB = decltype(&k_bf16_gemv_staged<8>);
+        const KB kb[8] = {k_bf16_gemv_staged<8>,  k_bf16_gemv_staged<16>, k_bf16_gemv_staged<24>,
+                          k_bf16_gemv_staged<32>, k_bf16_gemv_staged<40>, k_bf16_gemv_staged<48>,
+                          k_bf16_gemv_staged<56>, k_bf16_gemv_staged<64>};
+        kb[(cols / 64 - 1) / 8]<<<blocks, 256, (size_t)4 * 2 * (cols / 2) * 4, ctx->stream>>>(
+            (const float *)a.ptr(0), (const uint32_t *)a.ptr(1), (float *)a.ptr(2), cols, rr, off);
+        return launched(ctx);
+    }
     uint64_t total = (uint64_t)G[0] * G[1];
     k_bf16_project<<<blocks_for(total), 256, 0, ctx->stream>>>((const float *)a.ptr(0), (const uint32_t *)a.ptr(1),
                                                                (float *)a.ptr(2), cols, rows, tokens, stride, off,
@@ -572,6 +743,29 @@ int L_quant_gemv(sm_ctx *ctx, const uint32_t *G, Args a) {
     if (int rc = need(ctx, a.ptr(2), (elems / groupSize) * 4, "Scales")) return rc;
     if (hasOffset)
         if (int rc = need(ctx, a.ptr(3), (elems / groupSize) * 4, "Offsets")) return rc;
+    const int cw = cols * bits / 32, ng = cols / groupSize;
+    if (cols % 64 == 0 && cols <= 64 * kStagedMaxJ && cw % 4 == 0 && (groupSize & (groupSize - 1)) == 0 &&
+        ng <= 256 && a.ptr(1) % 16 == 0) {
+        // whole rows staged in LDS (same sums, same order)
+        int shift = 0;
+        while ((1 << shift) < groupSize) shift++;
+        const int bufw = cw + 2 * kStagedOffsets;
+        // rows per wave: up to kRowsPerWave, the block's buffers within 64 KiB
+        const int rpw = std::max(1, std::min(kRowsPerWave, 65536 / (4 * bufw * 4)));
+        const unsigned blocks = (unsigned)((rr + 4 * rpw - 1) / (4 * rpw));
+        const size_t lds = (size_t)4 * rpw * bufw * 4;
+        using KQ = decltype(&k_quant_gemv_staged<4, 8>);
+#define SM_QG_ROW(B)                                                                                               \
+    {k_quant_gemv_staged<B, 8>,  k_quant_gemv_staged<B, 16>, k_quant_gemv_staged<B, 24>, k_quant_gemv_staged<B, 32>, \
+     k_quant_gemv_staged<B, 40>, k_quant_gemv_staged<B, 48>, k_quant_gemv_staged<B, 56>, k_quant_gemv_staged<B, 64>}
+        const KQ kq[3][8] = {SM_QG_ROW(2), SM_QG_ROW(4), SM_QG_ROW(8)};
+#undef SM_QG_ROW
+        const KQ k = kq[bits == 2 ? 0 : bits == 4 ? 1 : 2][(cols / 64 - 1) / 8];
+        k<<<blocks, 256, lds, ctx->stream>>>((const float *)a.ptr(0), (const uint32_t *)a.ptr(1),
+                                             (const float *)a.ptr(2), (const float *)a.ptr(3), (float *)a.ptr(4),
+                                             cols, rr, shift, bias, codebook, hasOffset, rpw);
+        return launched(ctx);
+    }
     k_quant_project<<<blocks_for(G[0]), 256, 0, ctx->stream>>>(
         (const float *)a.ptr(0), (const uint32_t *)a.ptr(1), (const float *)a.ptr(2), (const float *)a.ptr(3),
         (float *)a.ptr(4), cols, rows, 1, rows, 0, bits, groupSize, bias, codebook, hasOffset, G[0], G[0]);

@@ -287,10 +287,12 @@ def test_bf16_project_quant_gemv_ple_decode_embed_rope(backend, oracle):
                     grid(100))
 
 
-@pytest.mark.parametrize("cols,rows,tokens", [(512, 9, 1), (4096, 5, 2), (300, 7, 2), (4608, 3, 1)])
+@pytest.mark.parametrize("cols,rows,tokens", [(512, 9, 1), (4096, 5, 2), (300, 7, 2), (4608, 3, 1), (2560, 70, 1),
+                                               (4096, 17, 1)])
 def test_bf16_project_shapes(backend, oracle, cols, rows, tokens):
     """Row widths that are and are not whole 512-value (eight-load) batches,
-    one and two tokens: the reference's bits in every case."""
+    one and two tokens, rows staged in LDS (one token, cols % 64 == 0, up
+    to 4096) and not: the reference's bits in every case."""
     rng = np.random.default_rng(cols)
     w = rng.normal(0, 0.05, rows * cols + 1).astype(np.float32)
     hi = (w.view(np.uint32) >> 16).astype(np.uint32)
@@ -304,12 +306,15 @@ def test_bf16_project_shapes(backend, oracle, cols, rows, tokens):
                                               Y=np.zeros(tokens * rows, np.float32)))
 
 
-@pytest.mark.parametrize("cols,bits,gs,has_offset", [(2560, 4, 32, 1), (2560, 8, 64, 0), (4096, 8, 16, 1),
-                                                      (96, 2, 32, 1), (4096, 2, 8, 0), (336, 4, 48, 1)])
-def test_quant_gemv_shapes(backend, oracle, cols, bits, gs, has_offset):
-    """S2 / S4 / S8 rows of 96 to 4096 values, groups of 8 to 64, with and
-    without offsets: the reference's bits in every case."""
-    rows = 11
+@pytest.mark.parametrize("cols,bits,gs,has_offset,codebook,rows",
+                         [(2560, 4, 32, 1, 0, 11), (2560, 8, 64, 0, 0, 11), (4096, 8, 16, 1, 0, 11),
+                          (96, 2, 32, 1, 0, 11), (4096, 2, 8, 0, 0, 11), (336, 4, 48, 1, 0, 11),
+                          (2560, 2, 128, 1, 0, 37), (1024, 4, 64, 1, 1, 53), (2560, 4, 32, 0, 1, 16)])
+def test_quant_gemv_shapes(backend, oracle, cols, bits, gs, has_offset, codebook, rows):
+    """S2 / S4 / S8 rows of 96 to 4096 values, groups of 8 to 128, with and
+    without offsets, the IQ4 codebook, rows staged in LDS (cols % 64 == 0,
+    whole 16-byte code chunks, power-of-two groups, at most 256 per row) and
+    not: the reference's bits in every case."""
     rng = np.random.default_rng(cols * bits + gs)
     cw = rng.integers(0, 2 ** 32, (cols * rows * bits + 31) // 32, dtype=np.uint64).astype(np.uint32)
     sc = rng.normal(0, 0.03, cols * rows // gs).astype(np.float32)
@@ -320,5 +325,5 @@ def test_quant_gemv_shapes(backend, oracle, cols, bits, gs, has_offset):
     backend.run("strata_quant_gemv", {"X": backend.alloc(xv), "Codes": backend.alloc(cw, "u32"),
                                       "Scales": backend.alloc(sc), "Offsets": backend.alloc(of), "Y": out,
                                       "cols": cols, "rows": rows, "bits": bits, "groupSize": gs, "bias": bias,
-                                      "codebook": 0, "hasOffset": has_offset}, [rows, 1, 1])
-    same(backend.read(out), oracle.quant_gemv(xv, cw, sc, of, cols, rows, bits, gs, bias, 0, has_offset))
+                                      "codebook": codebook, "hasOffset": has_offset}, [rows, 1, 1])
+    same(backend.read(out), oracle.quant_gemv(xv, cw, sc, of, cols, rows, bits, gs, bias, codebook, has_offset))
