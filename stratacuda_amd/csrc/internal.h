@@ -134,9 +134,9 @@ int route_launch(sm_ctx *ctx, const float *X, int tokens, int width, const float
 // fp16 MFMA, exact reference-order logits for the candidates near the top-k
 // boundary only, per-token certification with an exact fallback. IDs and
 // their order bit-exact, weights within a few ulp. route_cert_prepare
-// converts W_r (fp16, the split activations' K order) into the workspace;
-// route_cert_launch then needs the fp16 hi/lo split of X (k_split_hilo's
-// layout). Per-token stats (uint32 candidates | 1 << 16 on a fallback) at
+// converts W_r (fp16, the split activations' K order) into the workspace,
+// and with X given also writes X's fp16 hi/lo split to Xhl (k_split_hilo's
+// layout) in the same launch; route_cert_launch then needs that split. Per-token stats (uint32 candidates | 1 << 16 on a fallback) at
 // route_cert_stats_offset.
 // From 512 tokens on (graph replays of 8 layers on one MI355X, hidden 2048,
 // 512 experts, top-10: 384 tokens 253.5 us per layer certified against 253.1
@@ -146,7 +146,8 @@ constexpr int kRouteCertMinTokens = 512;
 bool route_cert_applies(int tokens, int width, int experts, int topk);
 uint64_t route_cert_workspace(int tokens, int width, int experts);
 uint64_t route_cert_stats_offset(int tokens, int width, int experts);
-int route_cert_prepare(sm_ctx *ctx, const float *Wr, int tokens, int width, int experts, char *ws);
+int route_cert_prepare(sm_ctx *ctx, const float *Wr, int tokens, int width, int experts, char *ws,
+                       const float *X = nullptr, _Float16 *Xhl = nullptr);
 int route_cert_launch(sm_ctx *ctx, const float *X, const _Float16 *Xhl, int tokens, int width, const float *Wr,
                       const float *bias, int experts, int topk, int *ids, float *weights, const float *gate_w,
                       float *gate_out, char *ws);

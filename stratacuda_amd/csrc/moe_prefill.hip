@@ -65,24 +65,7 @@ __device__ __forceinline__ int k_position(int r) {
 // X [rows x K] f32 -> hi/lo fp16 [rows][K/64][2][64] in the MFMA K order.
 __global__ void __launch_bounds__(256) k_split_hilo(const float *__restrict__ X, _Float16 *__restrict__ out,
                                                     int64_t groups) {
-    // Thread (group rg, chunk c) writes positions 8c .. 8c+7 of the group's
-    // hi and lo halves: elements 16w + 4h + {0, 8, 1, 9, 2, 10, 3, 11} with
-    // w = c / 2, h = c % 2, i.e. two float4 reads and two 16-byte writes.
-    const int64_t at = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t rg = at >> 3;
-    if (rg >= groups) return;
-    const int c = (int)(at & 7), src = 16 * (c >> 1) + 4 * (c & 1);
-    const float4 a = *(const float4 *)(X + rg * 64 + src), b = *(const float4 *)(X + rg * 64 + src + 8);
-    const float x[8] = {a.x, b.x, a.y, b.y, a.z, b.z, a.w, b.w};
-    half8 hi, lo;
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const _Float16 h = (_Float16)x[u];
-        hi[u] = h;
-        lo[u] = (_Float16)(x[u] - (float)h);
-    }
-    *(half8 *)(out + rg * 128 + 8 * c) = hi;
-    *(half8 *)(out + rg * 128 + 64 + 8 * c) = lo;
+    sm::split_hilo_chunk(X, out, (int64_t)blockIdx.x * blockDim.x + threadIdx.x, groups);
 }
 
 // The stack block's RMSNorm for small batches (kernels/strata.cu strata_norm
@@ -1126,7 +1109,11 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     // Other shapes: the split on the second stream, beside the router.
     const bool aux = !one_stream;  // the second stream holds work from here to the combine
     int rc = aux ? fork_aux(ctx) : SM_OK;
-    if (rc == SM_OK && !hilo_in_norm) {
+    // With the certified router on one stream the split rides in the router's
+    // preparation launch (route_cert_prepare) instead.
+    const bool cert = route_cert_applies(tokens, width, experts, topk);
+    const bool split_in_prep = cert && !aux && !hilo_in_norm;
+    if (rc == SM_OK && !hilo_in_norm && !split_in_prep) {
         const int64_t groups = (int64_t)tokens * (width / 64);
         k_split_hilo<<<(unsigned)((groups * 8 + 255) / 256), 256, 0, aux ? ctx->aux : ctx->stream>>>(
             (const float *)X, (_Float16 *)(ws + w.Xhl), groups);
@@ -1146,10 +1133,12 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     };
     auto wait_split = [ctx, aux]() { return aux ? wait_aux_mark(ctx) : SM_OK; };
     if (int rc2 = stage_mark(ctx, kStagePrefillRoute)) return bail(rc2);
-    if (route_cert_applies(tokens, width, experts, topk)) {
-        // The certified router: W_r's fp16 copy here while the second stream
-        // splits X, then the approximate logits from both.
-        if (int rc2 = route_cert_prepare(ctx, (const float *)Wr, tokens, width, experts, ws + w.rcert))
+    if (cert) {
+        // The certified router: W_r's fp16 copy (with X's split in the same
+        // launch, or on the second stream), then the approximate logits from
+        // both.
+        if (int rc2 = route_cert_prepare(ctx, (const float *)Wr, tokens, width, experts, ws + w.rcert,
+                                         split_in_prep ? (const float *)X : nullptr, (_Float16 *)(ws + w.Xhl)))
             return bail(rc2);
         if (int rc2 = wait_split()) return bail(rc2);
         if (int rc2 = route_cert_launch(ctx, (const float *)X, xhl, tokens, width, (const float *)Wr,

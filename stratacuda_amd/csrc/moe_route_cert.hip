@@ -67,12 +67,20 @@ constexpr uint32_t kCertFallback = 1u << 16;
 // row's squares. One block per row. The blocks also clear `nzero` words at
 // `zero` (the fallback list's count and per-token counters) for the
 // kernels after them.
+// Blocks from `experts` on (when X is given) write X's fp16 hi/lo split
+// instead (sm::split_hilo_chunk, 256 chunks per block): the two jobs are
+// independent and share one launch.
 __global__ void __launch_bounds__(256) k_route_prep_w(const float *__restrict__ Wr, _Float16 *__restrict__ Wh,
                                                       float *__restrict__ rn2, int width, int *__restrict__ zero,
-                                                      int nzero) {
+                                                      int nzero, int experts, const float *__restrict__ X,
+                                                      _Float16 *__restrict__ Xhl, int64_t groups) {
     __shared__ float s_part[4];
     const int e = blockIdx.x, tid = threadIdx.x;
-    for (int i = e * 256 + tid; i < nzero; i += gridDim.x * 256) zero[i] = 0;
+    if (e >= experts) {
+        sm::split_hilo_chunk(X, Xhl, (int64_t)(e - experts) * 256 + tid, groups);
+        return;
+    }
+    for (int i = e * 256 + tid; i < nzero; i += experts * 256) zero[i] = 0;
     const float *row = Wr + (int64_t)e * width;
     _Float16 *out = Wh + (int64_t)e * width;
     float ss = 0.0f;
@@ -755,10 +763,14 @@ uint64_t route_cert_stats_offset(int tokens, int width, int experts) {
     return cert_ws(tokens, width, experts).stats;
 }
 
-int route_cert_prepare(sm_ctx *ctx, const float *Wr, int tokens, int width, int experts, char *ws) {
+int route_cert_prepare(sm_ctx *ctx, const float *Wr, int tokens, int width, int experts, char *ws, const float *X,
+                       _Float16 *Xhl) {
     const CertWs w = cert_ws(tokens, width, experts);
-    k_route_prep_w<<<(unsigned)experts, 256, 0, ctx->stream>>>(Wr, (_Float16 *)(ws + w.Wh), (float *)(ws + w.rn2),
-                                                               width, (int *)(ws + w.fb), tokens + 1);
+    const int64_t groups = X ? (int64_t)tokens * (width / 64) : 0;
+    const unsigned split_blocks = (unsigned)((groups * 8 + 255) / 256);
+    k_route_prep_w<<<(unsigned)experts + split_blocks, 256, 0, ctx->stream>>>(
+        Wr, (_Float16 *)(ws + w.Wh), (float *)(ws + w.rn2), width, (int *)(ws + w.fb), tokens + 1, experts, X, Xhl,
+        groups);
     return launched(ctx);
 }
 

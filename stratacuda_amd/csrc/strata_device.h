@@ -844,4 +844,29 @@ __device__ __forceinline__ bool router_confirm(const float (&q)[8], int experts,
     return stood;
 }
 
+// One thread's part of the fp16 hi/lo split of X [rows x K] f32 into
+// [rows][K/64][2][64] in the expert GEMMs' K order (position q of a group
+// holds element 16 (q / 16) + (q / 2) % 8 + 8 (q % 2)): thread `at` (group
+// at / 8, chunk c = at % 8) writes positions 8c .. 8c+7 of the group's hi and
+// lo halves, i.e. elements 16w + 4h + {0, 8, 1, 9, 2, 10, 3, 11} with
+// w = c / 2, h = c % 2: two float4 reads and two 16-byte writes.
+__device__ __forceinline__ void split_hilo_chunk(const float *__restrict__ X, _Float16 *__restrict__ out, int64_t at,
+                                                 int64_t groups) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const int64_t rg = at >> 3;
+    if (rg >= groups) return;
+    const int c = (int)(at & 7), src = 16 * (c >> 1) + 4 * (c & 1);
+    const float4 a = *(const float4 *)(X + rg * 64 + src), b = *(const float4 *)(X + rg * 64 + src + 8);
+    const float x[8] = {a.x, b.x, a.y, b.y, a.z, b.z, a.w, b.w};
+    h8 hi, lo;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const _Float16 h = (_Float16)x[u];
+        hi[u] = h;
+        lo[u] = (_Float16)(x[u] - (float)h);
+    }
+    *(h8 *)(out + rg * 128 + 8 * c) = hi;
+    *(h8 *)(out + rg * 128 + 64 + 8 * c) = lo;
+}
+
 }  // namespace sm
