@@ -451,6 +451,17 @@ def _gemm_label(name):
     m = re.search(r"k_split_hilo", name)
     if m:
         return "k_split_hilo"
+    # a symbol the profiler left mangled (an anonymous-namespace kernel with
+    # integer / bool template arguments): its name and arguments
+    m = re.match(r"_ZN12_GLOBAL__N_1(\d+)", name)
+    if m:
+        rest = name[m.end():]
+        base = rest[:int(m.group(1))]
+        targs = re.match(r"I((?:L[ib]\d+E)+)E", rest[int(m.group(1)):])
+        if targs:
+            vals = re.findall(r"L([ib])(\d+)E", targs.group(1))
+            base += "<%s>" % ", ".join(("true" if v == "1" else "false") if k == "b" else v for k, v in vals)
+        return base
     return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
 
 
