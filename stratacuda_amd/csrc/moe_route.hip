@@ -354,12 +354,32 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_scan(const int *__res
 // The whole dispatch for up to kDispatchOneMaxBlocks token blocks (64
 // tokens each) in one block of SCAN_THREADS threads: the token masks of
 // every token block per expert in LDS, expert offsets by a block scan, the
-// per-block bases, the tilings and tile records, then the placement (same
-// results as masks + scan + place). experts <= 512.
+// tilings and tile records, then the placement (same results as masks +
+// scan + place). experts <= 512, tokens x topk + extra <= kDispatchOneRows.
 // Up to 512 tokens (A/B on one GPU, graph replays against masks + scan +
 // place: 128 tokens 154 -> 145 us per stack block, 256 tokens 191 -> 184,
-// T=512 unchanged).
+// T=512 unchanged). The rows and parts lists are built in LDS (token |
+// assignment << 16 per position) and written out in order: written
+// straight from each assignment, the stores scatter over the lists and the
+// block's single address unit took ~5.8 of the kernel's ~12.3 us at 512
+// tokens (timeline marks, -DSM_DISPATCH_TRACE). A row's first position in
+// its token block's part of the segment is the segment start plus the
+// expert's tokens in the blocks before (popcounts of their masks).
 constexpr int kDispatchOneMaxBlocks = 8;
+constexpr int kDispatchOnePerThread = 8;  // assignments per thread: tokens x topk <= SCAN_THREADS x 8
+constexpr int kDispatchOneRows = 7168;    // positions staged in LDS (512 tokens x top-13 + 512 shared)
+#ifdef SM_DISPATCH_TRACE
+// Timeline hook (profiling builds): thread 0 writes s_memrealtime (100 MHz) at mark k.
+__device__ uint64_t g_dispatch_trace[16];
+#define DISPATCH_MARK(k)                                                                   \
+    do {                                                                                   \
+        if (threadIdx.x == 0) g_dispatch_trace[k] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define DISPATCH_MARK(k) \
+    do {                 \
+    } while (0)
+#endif
 __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_one(const int *__restrict__ ids, int tokens, int topk,
                                                                int experts, int *__restrict__ offsets,
                                                                int *__restrict__ rows, int *__restrict__ parts,
@@ -370,16 +390,28 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_one(const int *__rest
                                                                int4 *__restrict__ info_small,
                                                                int4 *__restrict__ info_big) {
     __shared__ unsigned long long m[kDispatchOneMaxBlocks][512];  // [token block][expert] token masks
-    __shared__ int s_base[kDispatchOneMaxBlocks][512];            // first row of (token block, expert)
+    __shared__ uint32_t s_stage[kDispatchOneRows];                // position -> token | assignment << 16
     __shared__ int s_off[513];
     __shared__ int s_wave[SCAN_THREADS / 64];
     __shared__ uint32_t s_flags;
     const int tid = threadIdx.x, n = tokens * topk, nb = (tokens + 63) >> 6;
+    DISPATCH_MARK(0);
+    // The thread's assignments a = tid + SCAN_THREADS u: IDs loaded once, all
+    // at once (the placement uses them again).
+    int my_e[kDispatchOnePerThread];
+#pragma unroll
+    for (int u = 0; u < kDispatchOnePerThread; u++) {
+        const int a = tid + SCAN_THREADS * u;
+        my_e[u] = a < n ? ids[a] : -1;
+    }
     for (int i = tid; i < nb * 512; i += SCAN_THREADS) m[i >> 9][i & 511] = 0ull;
     if (tid == 0) s_flags = 0;
     __syncthreads();
-    for (int a = tid; a < n; a += SCAN_THREADS) {
-        const int e = ids[a];
+    DISPATCH_MARK(1);
+#pragma unroll
+    for (int u = 0; u < kDispatchOnePerThread; u++) {
+        const int a = tid + SCAN_THREADS * u, e = my_e[u];
+        if (a >= n) continue;
         if (e < 0 || e >= experts) {
             atomicOr(&s_flags, 1u);
             continue;
@@ -389,30 +421,32 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_one(const int *__rest
         if (atomicOr(&m[t >> 6][e], bit) & bit) atomicOr(&s_flags, 2u);
     }
     __syncthreads();
+    DISPATCH_MARK(2);
     const int e = tid;
     int tot = 0;
     if (e < experts)
-        for (int b = 0; b < nb; b++) {
-            s_base[b][e] = tot;
-            tot += __popcll(m[b][e]);
-        }
+        for (int b = 0; b < nb; b++) tot += __popcll(m[b][e]);
     const int incl = block_inclusive_scan(tot, s_wave), excl = incl - tot;
+    DISPATCH_MARK(3);
     if (e < experts) {
         offsets[e] = excl;
         s_off[e] = excl;
-        for (int b = 0; b < nb; b++) s_base[b][e] += excl;
         if (e == experts - 1) {
             offsets[experts] = incl;
             offsets[experts + 1] = incl + extra;
             s_off[experts] = incl;
         }
     }
+    // Tiles per segment, both kinds in one scan (small tiles in the low 16
+    // bits: at most kDispatchOneRows of them).
     const int cnt = e < experts ? tot : e == experts ? extra : 0;
     int ns = 0, nbg = 0;
     if (cnt >= split) nbg = (cnt + mt_big - 1) / mt_big;
     else ns = (cnt + mt_small - 1) / mt_small;
-    const int ts = block_inclusive_scan(ns, s_wave), tb = block_inclusive_scan(nbg, s_wave);
-    if (e == 0) *status = s_flags;  // block scans above synchronised the block
+    const int both = block_inclusive_scan(ns | (nbg << 16), s_wave);
+    const int ts = both & 0xffff, tb = both >> 16;
+    DISPATCH_MARK(4);
+    if (e == 0) *status = s_flags;  // the block scans above synchronised the block
     if (e <= experts) {
         tile_small[e + 1] = ts;
         tile_big[e + 1] = tb;
@@ -422,26 +456,36 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_one(const int *__rest
         if (info)
             for (int j = 0; j < cnt_t; j++) info[first + j] = make_int4(e, excl + j * mt, excl + cnt, excl);
     }
-    __syncthreads();  // s_off and s_base complete
-    for (int a = tid; a < n + (extra ? tokens : 0); a += SCAN_THREADS) {
-        if (a < n) {
-            const int t = a / topk, ex = ids[a];
-            if (ex < 0 || ex >= experts) {
-                where_[a] = -1;
-                continue;
-            }
-            const int tl = t & 63;
-            const unsigned long long below = tl ? (m[t >> 6][ex] & ((1ull << tl) - 1ull)) : 0ull;
-            const int pos = s_base[t >> 6][ex] + __popcll(below);
-            rows[pos] = t;
-            parts[pos] = a;
-            where_[a] = pos;
-        } else {
-            const int t = a - n, at = s_off[experts] + t;
-            rows[at] = t;
-            parts[at] = -1;
+    __syncthreads();  // s_off complete
+    DISPATCH_MARK(5);
+#pragma unroll
+    for (int u = 0; u < kDispatchOnePerThread; u++) {
+        const int a = tid + SCAN_THREADS * u, ex = my_e[u];
+        if (a >= n) continue;
+        if (ex < 0 || ex >= experts) {
+            where_[a] = -1;
+            continue;
         }
+        const int t = a / topk, tb6 = t >> 6, tl = t & 63;
+        int pos = s_off[ex] + (tl ? __popcll(m[tb6][ex] & ((1ull << tl) - 1ull)) : 0);
+        for (int b = 0; b < tb6; b++) pos += __popcll(m[b][ex]);
+        s_stage[pos] = (uint32_t)t | ((uint32_t)a << 16);
+        where_[a] = pos;
     }
+    if (extra)
+        for (int t = tid; t < tokens; t += SCAN_THREADS) s_stage[s_off[experts] + t] = (uint32_t)t | 0xffff0000u;
+    __syncthreads();
+    DISPATCH_MARK(6);
+    const int total = s_off[experts] + (extra ? tokens : 0);
+    for (int p = tid; p < total; p += SCAN_THREADS) {
+        const uint32_t v = s_stage[p];
+        rows[p] = (int)(v & 0xffffu);
+        parts[p] = (v >> 16) == 0xffffu ? -1 : (int)(v >> 16);
+    }
+#ifdef SM_DISPATCH_TRACE
+    __syncthreads();
+    DISPATCH_MARK(7);
+#endif
 }
 
 __global__ void k_dispatch_place(const int *__restrict__ ids, int tokens, int topk, int experts, int nb,
@@ -568,7 +612,8 @@ int dispatch_launch(sm_ctx *ctx, const int *ids, int tokens, int topk, int exper
     const uint64_t n = (uint64_t)tokens * topk, extra = extra_rows ? (uint64_t)tokens : 0;
     GemmTiling none = {(int *)(ws + w.tile_small), (int *)(ws + w.tile_big), 64, 32, 128};
     const GemmTiling &tl = tiling ? *tiling : none;
-    if (nb <= kDispatchOneMaxBlocks && experts <= 512) {
+    if (nb <= kDispatchOneMaxBlocks && experts <= 512 && n <= (uint64_t)SCAN_THREADS * kDispatchOnePerThread &&
+        n + extra <= (uint64_t)kDispatchOneRows) {
         k_dispatch_one<<<1, SCAN_THREADS, 0, ctx->stream>>>(ids, tokens, topk, experts, offsets, rows, parts, where_,
                                                             (int)extra, tl.small, tl.big, tl.split, tl.mt_small,
                                                             tl.mt_big, (uint32_t *)(ws + w.status),
@@ -607,3 +652,11 @@ int dispatch(sm_ctx *ctx, uint64_t ids, int tokens, int topk, int experts, uint6
 }
 
 }  // namespace smi
+
+#ifdef SM_DISPATCH_TRACE
+extern "C" int sm_dispatch_trace_read(uint64_t *out, int n) {
+    if (n < 16) return SM_E_ARG;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_dispatch_trace), sizeof(uint64_t) * 16) == hipSuccess ? SM_OK
+                                                                                                      : SM_E_HIP;
+}
+#endif
