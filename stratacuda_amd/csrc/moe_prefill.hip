@@ -907,50 +907,47 @@ __global__ void __launch_bounds__(256, 3) k_moe_gemm_rows16(const _Float16 *__re
 
 // Y[t, d] = P[shared(t), d] * sigmoid(gate[t]) + sum_k P[where[t,k], d] * w[t,k]
 // in the reference order (kernels/strata.cu:470-476); with `resid`,
-// Y = resid + that (strata_elementwise mode 5). One block per token:
-// the token's slot positions, weights and sigmoid(gate) are read once, then
-// each thread combines 4 consecutive outputs per step with 16-byte loads.
-// Needs width % 4 == 0.
-constexpr int COMBINE_MAX_K = 32;
+// Y = resid + that (strata_elementwise mode 5). One block per token (and
+// column block): each thread combines 4 consecutive outputs per step with
+// 16-byte loads. Needs width % 4 == 0 (topk <= 32, checked by the caller's
+// geometry check).
 __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, const int *__restrict__ where_,
                                                  const float *__restrict__ weights, const float *__restrict__ gate,
                                                  int64_t shared_base, float *__restrict__ Y, int tokens,
                                                  int topk, int width, const float *__restrict__ resid) {
-    __shared__ int s_pos[COMBINE_MAX_K];
-    __shared__ float s_w[COMBINE_MAX_K];
-    __shared__ float s_sig;
+    // The token's slot positions, weights and gate are the same for every
+    // thread of the block (scalar loads), and the parts of up to
+    // kCombineRound slots are loaded before any is added (in slot order), so
+    // a top-10 token waits for one round of loads.
+    constexpr int kCombineRound = 16;
     const int t = blockIdx.x, tid = threadIdx.x;
-    if (tid < topk) {
-        s_pos[tid] = where_[(int64_t)t * topk + tid];
-        s_w[tid] = weights[(int64_t)t * topk + tid];
-    }
-    if (tid == 0) s_sig = sm::sigmoid(gate[t]);
-    __syncthreads();
-    const float sig = s_sig;
+    const int *wt = where_ + (int64_t)t * topk;
+    const float *ww = weights + (int64_t)t * topk;
+    const float sig = sm::sigmoid(gate[t]);
     const float4 *shared_row = (const float4 *)(P + (shared_base + t) * width);
     // block (t, c) covers float4 columns c x 256 + tid, in steps of the
     // grid's column extent
     for (int d4 = blockIdx.y * blockDim.x + tid; d4 < width / 4; d4 += blockDim.x * gridDim.y) {
         const float4 s = shared_row[d4];
         float4 v = {s.x * sig, s.y * sig, s.z * sig, s.w * sig};
-        // the parts of up to eight slots are loaded before any is added (in
-        // slot order)
-        for (int k0 = 0; k0 < topk; k0 += 8) {
-            float4 part[8];
+        for (int k0 = 0; k0 < topk; k0 += kCombineRound) {
+            float4 part[kCombineRound];
+            float w[kCombineRound];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int pos = k0 + j < topk ? s_pos[k0 + j] : -1;
+            for (int j = 0; j < kCombineRound; j++) {
+                const int pos = k0 + j < topk ? wt[k0 + j] : -1;
+                w[j] = k0 + j < topk ? ww[k0 + j] : 0.0f;
                 part[j] = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
                 if (pos >= 0) part[j] = ((const float4 *)(P + (int64_t)pos * width))[d4];
             }
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                if (k0 + j >= topk) break;
-                const float w = s_w[k0 + j];
-                v.x = v.x + part[j].x * w;
-                v.y = v.y + part[j].y * w;
-                v.z = v.z + part[j].z * w;
-                v.w = v.w + part[j].w * w;
+            for (int j = 0; j < kCombineRound; j++) {
+                if (k0 + j < topk) {
+                    v.x = v.x + part[j].x * w[j];
+                    v.y = v.y + part[j].y * w[j];
+                    v.z = v.z + part[j].z * w[j];
+                    v.w = v.w + part[j].w * w[j];
+                }
             }
         }
         if (resid) {
