@@ -27,11 +27,12 @@
 //    (p, p+8) of word w come out of the code unpacking, so B needs no
 //    shuffle; the activations are stored in the same order, so staging them
 //    into LDS is a plain 16-byte copy and the MFMA A operand one 16-byte read.
-//  * Tiles (width and ff among 512 / 2048, the benchmark shapes): segments of
-//    more than 32 rows run in 64 x 256 blocks on v_mfma_f32_32x32x16_f16
-//    (k_moe_gemm_stream), shorter ones in 16 x 256 blocks on
-//    v_mfma_f32_16x16x32_f16 (k_moe_gemm_rows16, k_moe_gemm_stream16); the
-//    two grids cover disjoint rows and run on two streams. Each block reads
+//  * Tiles (width and ff among 512 / 2048, the benchmark shapes): below 1,024
+//    tokens every segment runs in 16 x 256 blocks on v_mfma_f32_16x16x32_f16
+//    (k_moe_gemm_rows16, k_moe_gemm_stream16), one grid; from 1,024 tokens
+//    segments of more than 32 rows run in 64 x 256 blocks on
+//    v_mfma_f32_32x32x16_f16 (k_moe_gemm_stream), the two grids covering
+//    disjoint rows and running on two streams. Each block reads
 //    its tile record (segment, first row, end row, segment start) written by
 //    the dispatch, which tiles the shared expert's segment (every token) with
 //    the routed ones.
@@ -961,17 +962,24 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ P, co
 constexpr uint64_t kAlign = 256;
 inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Batches of up to kSmallBatch tokens tile every segment (at most `tokens`
-// rows) in 16-row tiles, so the 64-row grid is not launched; larger ones
-// tile segments of more than 32 rows in 64-row tiles.
+// Batches of fewer than kOneGridTokens tokens tile every segment (at most
+// `tokens` rows: a token routes to an expert once, and the shared segment
+// holds each token once) in 16-row tiles, so the 64-row grid is not launched
+// and the products need no second stream; larger ones tile segments of more
+// than 32 rows in 64-row tiles, on the second stream beside the 16-row grid.
+// (Graph replays on one GPU, the 64-row grid forked beside the 16-row one
+// against one grid: 512 tokens, uniform routing, 0.261-0.268 -> 0.229-0.239
+// ms per layer; stack blocks of 128 / 256 / 512 tokens 144 / 185 / 225 ->
+// 126 / 165 / 211 us.)
+constexpr int kOneGridTokens = 1024;
 constexpr int kSmallBatch = 64;
 constexpr int kSmallBatchColumnTiles = 2;  // column tiles per wave of the 16-row kernel up to kSmallBatch tokens
-inline int tiling_split(int tokens) { return tokens <= kSmallBatch ? kSmallBatch + 1 : 33; }
+inline int tiling_split(int tokens) { return tokens < kOneGridTokens ? tokens + 1 : 33; }
 
 // Grid bounds of the two tilings over the experts + 1 segments of m rows:
 // a segment of r < split rows takes ceil(r / 16) <= r / 16 + 1 small tiles
-// (at most two when split is 33); a longer one ceil(r / 64) big tiles, in
-// all at most m / 64 + (number of such segments <= m / 33).
+// (at most two when split is 33 or less); a longer one ceil(r / 64) big
+// tiles, in all at most m / 64 + (number of such segments <= m / 33).
 inline uint64_t small_tile_bound(uint64_t m, int experts, int split) {
     const uint64_t segs = (uint64_t)experts + 1;
     const uint64_t any = m / 16 + std::min(segs, m) + 1;
@@ -1167,7 +1175,7 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     auto round8 = [](uint64_t v) { return (unsigned)((v + 7) / 8 * 8); };
     const unsigned big_tiles = stream ? round8(big_tile_bound(m, experts)) : (unsigned)big_tile_bound(m, experts);
     const unsigned small_tiles = stream ? round8(small_tile_bound(m, experts, split)) : (unsigned)(segs + 1);
-    const bool any_big = split <= 33;  // otherwise no segment reaches the big tiling
+    const bool any_big = split <= tokens;  // otherwise no segment reaches the big tiling
     const int *rows = (const int *)(ws + w.rows);
     auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
                      void *out, int ld) -> int {

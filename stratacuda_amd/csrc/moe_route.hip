@@ -331,11 +331,11 @@ __global__ void __launch_bounds__(SCAN_THREADS) k_dispatch_scan(const int *__res
     int ns = 0, nbg = 0;
     if (cnt >= split) nbg = (cnt + mt_big - 1) / mt_big;
     else ns = (cnt + mt_small - 1) / mt_small;
-    // Both kinds in one scan while the counts fit 16 and 15 bits (small
-    // tiles: at most 4 per segment; big tiles: at most rows / 64 + segments,
-    // rows <= 64 nb x 32 + extra), else one scan each.
+    // Both kinds in one scan while the counts fit 16 and 15 bits (at most
+    // rows / 16 + segments small and rows / 64 + segments big tiles, rows <=
+    // 64 nb x 32 + extra), else one scan each.
     int ts, tb;
-    if ((int64_t)nb * 32 + extra / 64 + experts + 1 < 32768) {
+    if ((int64_t)nb * 128 + extra / 16 + experts + 1 < 32768) {
         const int both = block_inclusive_scan(ns | (nbg << 16), s_wave);
         ts = both & 0xffff;
         tb = both >> 16;

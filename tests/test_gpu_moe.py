@@ -242,8 +242,8 @@ def test_layer_routing_edge_logits(backend, oracle, full_layer, tokens):
 @pytest.mark.parametrize("tokens", [5, 6, 7, 16, 17, 24, 25, 40, 64, 65])
 def test_layer_small_batch_full(backend, oracle, full_layer, tokens):
     # 5 and 6 tokens: the decode kernels with a token dimension (one top-k
-    # kernel for the batch); 7..64: 16-row tiles over every segment on one
-    # stream; 65: the first batch with 64-row tiles.
+    # kernel for the batch); 7..64: 16-row tiles of 128 weight rows over every
+    # segment; 65: the first batch with 256 weight rows per 16-row tile.
     check_full_layer(backend, oracle, full_layer, tokens, False)
 
 
@@ -251,7 +251,10 @@ def test_layer_small_batch_full(backend, oracle, full_layer, tokens):
                                                (512, 2048, 12, 3, 100), (2048, 512, 20, 4, 48),
                                                # the real model's widths: 40 and 10 groups
                                                (2560, 640, 20, 4, 70), (2048, 640, 16, 3, 48),
-                                               (2560, 512, 16, 3, 40)])
+                                               (2560, 512, 16, 3, 40),
+                                               # 1,024 tokens and more: 64-row tiles for 8, 10, 32
+                                               # and 40 groups beside the 16-row grid
+                                               (512, 2048, 12, 3, 1024), (2560, 640, 20, 4, 1024)])
 def test_layer_stream_geometries(backend, oracle, W, F, E, topk, tokens):
     # Every (width, ff) pair of the streaming kernels, with and without the
     # K split, against the oracle on all tokens.
