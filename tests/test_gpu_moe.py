@@ -195,6 +195,15 @@ def test_layer_prefill_2048_zipf_full(backend, oracle, full_layer):
     check_full_layer(backend, oracle, full_layer, 2048, True)
 
 
+@pytest.mark.parametrize("tokens,bias", [(700, True), (1023, False)])
+def test_layer_prefill_one_grid_full(backend, oracle, full_layer, tokens, bias):
+    # Past the one-block dispatch (512 tokens) and below 1,024 tokens: the
+    # masks / scan / place dispatch with every segment in 16-row tiles, the
+    # Zipf-biased router's hot experts (hundreds of rows) and the shared
+    # expert's segment (one row per token) included.
+    check_full_layer(backend, oracle, full_layer, tokens, bias)
+
+
 def routing_styles(E):
     x = np.arange(E)
     styles = {"ties": np.full(E, 7, np.float32),
