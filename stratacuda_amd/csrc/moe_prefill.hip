@@ -1041,8 +1041,10 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
         return fail(ctx, SM_E_ARG, "prefill needs width and 2*ff to be multiples of 128");
     // Streaming kernels: N a multiple of 256 and K one of the compiled group
     // counts in both products (512, 640, 2048, 2560: the benchmark's and the
-    // real model's shapes). Segments of up to 32 rows then run in 16-row
-    // tiles, else in one 32-row tile; longer ones in 64-row tiles.
+    // real model's shapes). Every segment then runs in 16-row tiles below
+    // kOneGridTokens tokens; from there on segments of up to 32 rows do, and
+    // longer ones run in 64-row tiles. Other shapes: segments of up to 32
+    // rows in one 32-row tile, longer ones in 64-row tiles (k_moe_gemm).
     auto streamable = [](int k) { return k == 512 || k == 640 || k == 2048 || k == 2560; };
     const bool stream = (2 * ff) % 256 == 0 && width % 256 == 0 && streamable(width) && streamable(ff);
     // Streaming shapes issue the split, the router and the dispatch on the
@@ -1180,9 +1182,9 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     auto gemms = [&](bool gate_up, const _Float16 *a, const int *r, int K, int N, uint64_t codes, uint64_t scales,
                      void *out, int ld) -> int {
         if (stream) {
-            // The two tilings cover disjoint rows: the big-tile grid (few,
-            // long blocks at small T) runs on the second stream beside the
-            // small-tile grid (after the shared expert's products there).
+            // The two tilings cover disjoint rows: the big-tile grid (from
+            // kOneGridTokens tokens on) runs on the second stream beside the
+            // small-tile grid.
             int rc_big = SM_OK;
             if (any_big) {
                 if (int rc3 = fork_aux(ctx)) return rc3;
@@ -1224,8 +1226,8 @@ int moe_prefill(sm_ctx *ctx, uint64_t X, int tokens, uint64_t Wr, uint64_t bias,
     if (int rc2 = gemms(true, xhl, rows, width, 2 * ff, L.gate_up_codes, L.gate_up_scales, ws + w.Hhl, ff)) return bail(rc2);
     if (int rc2 = stage_mark(ctx, kStagePrefillDown)) return bail(rc2);
     if (int rc2 = gemms(false, hhl, nullptr, ff, width, L.down_codes, L.down_scales, ws + w.P, width)) return bail(rc2);
-    // Everything on the second stream (the shared expert's products) is in
-    // before the combine reads P.
+    // Everything on the second stream (other shapes' split) is in before
+    // the combine reads P.
     if (aux)
         if (int rc2 = join_aux(ctx)) return rc2;
     if (int rc2 = stage_mark(ctx, kStagePrefillCombine)) return rc2;
