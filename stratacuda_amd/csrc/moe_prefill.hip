@@ -970,7 +970,10 @@ inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // (Graph replays on one GPU, the 64-row grid forked beside the 16-row one
 // against one grid: 512 tokens, uniform routing, 0.261-0.268 -> 0.229-0.239
 // ms per layer; stack blocks of 128 / 256 / 512 tokens 144 / 185 / 225 ->
-// 126 / 165 / 211 us.)
+// 126 / 165 / 211 us. From 1,024 tokens one grid loses once the router is
+// skewed: 1,024 tokens with a Zipf-biased router 0.277 -> 0.302 ms, 1,536
+// tokens 0.372 -> 0.415 ms; with uniform routing 0.373 -> 0.365 and 0.460 ->
+// 0.465 ms.)
 constexpr int kOneGridTokens = 1024;
 constexpr int kSmallBatch = 64;
 constexpr int kSmallBatchColumnTiles = 2;  // column tiles per wave of the 16-row kernel up to kSmallBatch tokens
